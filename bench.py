@@ -1,0 +1,221 @@
+"""Batch-one Qwen3 greedy decode throughput on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-8b]
+
+Default workload: the Qwen3-0.6B shape (hidden 1024, 28 layers, 16 q / 8 kv
+heads, head_dim 128, FFN 3072, vocab 151936, tied), random-init bf16
+weights N(0, 0.02), a 512-token uniform-random prompt, then K greedy decode
+steps (K = 64: context 512 -> 575). A step is one replay of the captured
+decode graph; the timed region replays K steps back to back with weights,
+KV cache and token/position state already resident in HBM.
+
+Also reported on the same line:
+  roofline      the dominant kernel (the fused RMSNorm + gate/up GEMV + SwiGLU,
+                one launch per layer), timed alone with HIP events on its stream
+                over rotating per-layer weights (28 x 12.6 MB, more than the
+                256 MB Infinity Cache), as algorithmic bytes / launch time;
+  decode_roofline  bytes per generated token / step time against 8 TB/s;
+  cpu_baseline  the CPU oracle (torch eager, this host's cores) on a bounded
+                sample of the same workload: batched prompt prefill + 8 greedy
+                decode steps, reported as decode tok/s;
+  qwen3_8b      the Qwen3-8B shape (untied), prompt 2048, 256 greedy steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from hackthenorth_amd import decode as D  # noqa: E402
+from hackthenorth_amd.kernels import projection as P  # noqa: E402
+from hackthenorth_amd.kernels import rng as DR  # noqa: E402
+from hackthenorth_amd.model import Qwen3Model, shape_config  # noqa: E402
+
+METRIC = "batch-1 decode tok/s at Qwen3 shapes + per-kernel HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+PROMPT_SEED, PROMPT_STREAM = 1, 7
+
+
+def kv_bytes_per_token(cfg, ctx):
+    """KV read over ctx slots plus the appended slot, all layers (bf16)."""
+    per_slot = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
+    return per_slot * (ctx + 1)
+
+
+def run_decode(shape, prompt_len, steps, warmup, log):
+    cfg = shape_config(shape)
+    model = Qwen3Model.random(cfg)
+    prompt = DR.randint(prompt_len, cfg.vocab_size, PROMPT_SEED, PROMPT_STREAM)
+    total = warmup + steps + 1
+    with torch.inference_mode():
+        state = D.DecodeState(model, 1, prompt_len, total)
+        t0 = time.perf_counter()
+        first = state.prefill(model, prompt.view(1, -1)).clone()
+        torch.cuda.synchronize()
+        log(f"{shape}: prefill of {prompt_len} tokens (step by step) {time.perf_counter() - t0:.2f}s")
+        for _ in range(warmup):
+            state.graph.replay()
+        # Time exactly `steps` decode steps from the state right after prefill.
+        state.position.fill_(prompt_len)
+        state.token.copy_(first)
+        tokens = torch.empty(steps, dtype=torch.int64, device=model.device)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for i in range(steps):
+            state.graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+        # Token ids of the timed run (one more pass, copying each token out).
+        state.position.fill_(prompt_len)
+        state.token.copy_(first)
+        for i in range(steps):
+            state.graph.replay()
+            tokens[i:i + 1].copy_(state.token[0])
+        torch.cuda.synchronize()
+    weights = model.weight_bytes()
+    mean_ctx = prompt_len + (steps - 1) / 2.0
+    bytes_per_token = weights + kv_bytes_per_token(cfg, mean_ctx)
+    tok_s = steps / elapsed
+    return dict(model=model, cfg=cfg, prompt=prompt.cpu().tolist(), first=int(first),
+                tokens=tokens.cpu().tolist(), elapsed=elapsed, tok_s=tok_s,
+                ms_per_step=1e3 * elapsed / steps, bytes_per_token=bytes_per_token,
+                decode_frac=bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9))
+
+
+def dominant_kernel(model, launches=280):
+    """Fused norm + gate/up + SwiGLU GEMV over the layers' weights, HIP events on its stream."""
+    cfg = model.config
+    layers = model.layers
+    x = torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16, device=model.device)
+    DR.normal_(x, 3, 99, 1.0)
+    gain = layers[0].post_attention_layernorm.weight
+    for layer in layers[:4]:
+        P.norm_projection(x, gain, layer.gate_up_weight, 1e-6, swiglu=True)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(launches):
+        P.norm_projection(x, gain, layers[i % len(layers)].gate_up_weight, 1e-6, swiglu=True)
+    end.record(stream)
+    end.synchronize()
+    avg_s = start.elapsed_time(end) / 1e3 / launches
+    k, n2 = cfg.hidden_size, 2 * cfg.intermediate_size
+    algorithmic = n2 * k * 2 + k * 2 * 2 + cfg.intermediate_size * 2  # W + x + gain + y
+    achieved = algorithmic / avg_s / 1e9
+    return dict(name="gemv_vec<norm, swiglu> (RMSNorm + gate/up GEMV + SwiGLU)",
+                avg_us=avg_s * 1e6, bytes=algorithmic, achieved=achieved)
+
+
+def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
+    from oracle import qwen3 as Q
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    shape = Q.SHAPES["0.6b"]
+    weights = Q.generate_weights(shape, seed=0)
+    oracle = Q.Oracle(shape, weights, capacity=len(prompt) + decode_steps + 1)
+    cache = Q.new_cache(shape, oracle.capacity)
+    ids = torch.tensor([prompt], dtype=torch.int64)
+    t0 = time.perf_counter()
+    tok, _, _ = oracle.forward(ids, cache, torch.arange(len(prompt)))
+    prefill_s = time.perf_counter() - t0
+    tokens = [int(tok[0, 0])]
+    t0 = time.perf_counter()
+    for i in range(decode_steps):
+        pos = torch.tensor([len(prompt) + i])
+        tok, _, _ = oracle.forward(torch.tensor([[tokens[-1]]]), cache, pos)
+        tokens.append(int(tok[0, 0]))
+    decode_s = time.perf_counter() - t0
+    agree = tokens[0] == first_gpu and tokens[1:] == steps_gpu_tokens[:decode_steps]
+    cpu_name = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_name = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": decode_steps / decode_s, "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"CPU oracle (torch eager, bf16 rounding of the reference path) on the same "
+                      f"0.6B workload: one batched prefill of the {len(prompt)}-token prompt "
+                      f"({prefill_s:.1f}s) then {decode_steps} greedy decode steps at ctx "
+                      f"{len(prompt)}-{len(prompt) + decode_steps - 1}; tok/s over the decode steps",
+            "prefill_s": round(prefill_s, 3), "tokens_match_gpu": bool(agree),
+            "cpu_model": cpu_name, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-8b", action="store_true")
+    ap.add_argument("--quiet", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the batch-one decode path on exactly one GPU; "
+              "multi-GPU runs are not part of this build", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(2)
+
+    def log(msg):
+        if not args.quiet:
+            print(msg, file=sys.stderr, flush=True)
+
+    res = run_decode("qwen3-0.6b", args.prompt, args.steps, args.warmup, log)
+    log(f"qwen3-0.6b: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step")
+    dom = dominant_kernel(res["model"])
+    log(f"dominant kernel: {dom['avg_us']:.2f} us/launch, {dom['achieved']:.0f} GB/s")
+    line = {
+        "metric": METRIC, "value": round(res["tok_s"], 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights and uniform prompt ids from the "
+                "counter RNG (seed 0 weights, seed 1 prompt)",
+        "config": {"workload": "Qwen3-0.6B-shape bf16 batch-1 greedy decode, prompt "
+                               f"{args.prompt}, {args.steps} steps (context {args.prompt}-"
+                               f"{args.prompt + args.steps - 1}), captured HIP graph per step",
+                   "batch": 1, "prompt_tokens": args.prompt, "decode_steps": args.steps},
+        "roofline": {"bound": "hbm", "achieved": round(dom["achieved"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": dom["name"], "avg_launch_us": round(dom["avg_us"], 3),
+                     "bytes_per_launch": dom["bytes"]},
+        "decode_roofline": {"bytes_per_token": res["bytes_per_token"],
+                            "achieved_GBs": round(res["bytes_per_token"] * res["tok_s"] / 1e9, 1),
+                            "frac": round(res["decode_frac"], 4),
+                            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / res["bytes_per_token"], 1)},
+        "first_tokens": [res["first"]] + res["tokens"][:15],
+    }
+    del res["model"]
+    torch.cuda.empty_cache()
+    if not args.no_8b:
+        try:
+            r8 = run_decode("qwen3-8b", 2048, 256, args.warmup, log)
+            del r8["model"]
+            torch.cuda.empty_cache()
+            line["qwen3_8b"] = {"workload": "Qwen3-8B-shape bf16, prompt 2048, 256 greedy steps",
+                                "tok_s": round(r8["tok_s"], 2),
+                                "ms_per_step": round(r8["ms_per_step"], 4),
+                                "bytes_per_token": r8["bytes_per_token"],
+                                "roofline_frac": round(r8["decode_frac"], 4),
+                                "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r8["bytes_per_token"], 1)}
+            log(f"qwen3-8b: {r8['tok_s']:.1f} tok/s ({100 * r8['decode_frac']:.1f}% of roofline)")
+        except Exception as exc:  # report, do not lose the headline line
+            line["qwen3_8b"] = {"error": repr(exc)}
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(res["prompt"], res["tokens"], res["first"])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

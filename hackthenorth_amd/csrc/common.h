@@ -1,0 +1,145 @@
+// Shared device helpers for the gfx950 decode kernels.
+//
+// bf16 values travel as raw 16-bit patterns; conversions are explicit so every
+// rounding boundary of the decode path is visible in the kernel source.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/htn_decode.h"
+
+namespace htn {
+
+typedef uint16_t bf16_t;
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // four waves
+
+// ------------------------------------------------------------------ bf16
+
+__device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch and the reference use).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return f2bf(lo) | (f2bf(hi) << 16);
+}
+
+// 8 bf16 in a uint4 -> fp32 dot with 8 fp32 values.
+__device__ __forceinline__ float dot8(uint4 w, const float* x) {
+  float s = bf_lo(w.x) * x[0];
+  s = fmaf(bf_hi(w.x), x[1], s);
+  s = fmaf(bf_lo(w.y), x[2], s);
+  s = fmaf(bf_hi(w.y), x[3], s);
+  s = fmaf(bf_lo(w.z), x[4], s);
+  s = fmaf(bf_hi(w.z), x[5], s);
+  s = fmaf(bf_lo(w.w), x[6], s);
+  s = fmaf(bf_hi(w.w), x[7], s);
+  return s;
+}
+
+__device__ __forceinline__ void unpack8(uint4 v, float* o) {
+  o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
+  o[4] = bf_lo(v.z); o[5] = bf_hi(v.z); o[6] = bf_lo(v.w); o[7] = bf_hi(v.w);
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte load of weights that are read exactly once per launch.
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ------------------------------------------------------------------ wave64 reductions
+// DPP row operations act on 16-lane rows; the four row results are combined
+// with readlane, so the total is wave-uniform. All 64 lanes must be active.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x128>(v);  // row_ror:8
+  return v;
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x124>(v));
+  v = fmaxf(v, dpp<0x128>(v));
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    uint64_t o = __shfl_xor(v, m, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Block-wide sum for 256 threads; `red` holds at least 4 floats of LDS.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+// Order-preserving key for (bf16 logit, vocabulary id): the larger logit wins,
+// and among equal logits the lower id wins. -0 is folded into +0 so that the
+// two zeros compare equal, as they do in torch.argmax.
+__device__ __forceinline__ uint64_t argmax_key(uint32_t bits16, uint32_t index) {
+  if (bits16 == 0x8000u) bits16 = 0;
+  uint32_t ord = (bits16 & 0x8000u) ? (~bits16 & 0xffffu) : (bits16 | 0x8000u);
+  return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(0xffffffffu - index);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
+  return 0xffffffffu - static_cast<uint32_t>(key & 0xffffffffu);
+}
+
+// ------------------------------------------------------------------ host helpers
+
+int device_cus();  // compute units of the current device (cached per device)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? HTN_OK : HTN_ELAUNCH;
+}
+
+}  // namespace htn

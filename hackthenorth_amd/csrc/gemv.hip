@@ -1,0 +1,375 @@
+// Batch-one GEMV family for gfx950: norm/QKV, norm/gate-up/SwiGLU, O/down +
+// residual, and the fused final-norm/LM-head/argmax greedy head.
+//
+// Design (HBM-bound, ~1 FLOP per weight byte):
+//  * one wave64 owns R output rows (R gate/up row pairs for SwiGLU) and walks
+//    the whole K extent, so the dot product finishes with one in-wave DPP
+//    reduction and no LDS traffic;
+//  * every lane issues 16-byte non-temporal loads, U chunks of 1 KB per row
+//    in flight per wave (U * R * S loads per lane), so a CU holds tens of KB
+//    of outstanding HBM reads;
+//  * the activation row (optionally RMS-normalised, rounded exactly as the
+//    reference) is staged once per block in LDS and read back with 16-byte
+//    LDS reads;
+//  * blocks grid-stride over row groups, so the prologue is paid once per
+//    block and the grid is sized to the CU count.
+#include "common.h"
+
+namespace htn {
+
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+// LDS layout: [0, 64) argmax keys of the four waves, [64, 128) reduction
+// scratch, then the staged activation row.
+constexpr int kLdsHead = 128;
+
+struct GemvArgs {
+  const bf16_t* x;
+  const bf16_t* gain;
+  const bf16_t* w;
+  const bf16_t* res;
+  bf16_t* y;
+  int64_t* token_out;
+  int64_t* position_inc;
+  uint64_t* slot;      // argmax key (sync buffer)
+  unsigned* counter;   // blocks finished (sync buffer)
+  long n;              // output rows (gate rows for SwiGLU)
+  int k;
+  int kpad;            // k rounded up to 512
+  float eps;
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // bf16(bf16(g * sigmoid(g)) * u), sigmoid = 1 / (1 + exp(-g)), each op rounded in fp32.
+  float sig = 1.0f / (1.0f + expf(-g));
+  float act = round_bf(g * sig);
+  return act * u;
+}
+
+// Stage x (or its RMSNorm) into LDS as bf16, zero-padded to kpad.
+template <bool NORM>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, bf16_t* xs, float* red) {
+  const int tid = threadIdx.x;
+  const int kv = a.k >> 3, kvp = a.kpad >> 3;
+  float ss = 0.f;
+  for (int v = tid; v < kvp; v += kBlock) {
+    uint4 xv = make_uint4(0, 0, 0, 0);
+    if (v < kv) xv = *reinterpret_cast<const uint4*>(a.x + v * 8);
+    if (NORM) {
+      float f[8];
+      unpack8(xv, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+    *reinterpret_cast<uint4*>(xs + v * 8) = xv;
+  }
+  if (NORM) {
+    const float total = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(a.k) + a.eps);
+    for (int v = tid; v < kv; v += kBlock) {
+      float f[8], g[8];
+      unpack8(*reinterpret_cast<const uint4*>(xs + v * 8), f);
+      unpack8(*reinterpret_cast<const uint4*>(a.gain + v * 8), g);
+      uint4 o;
+      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+      *reinterpret_cast<uint4*>(xs + v * 8) = o;
+    }
+  }
+  __syncthreads();
+}
+
+// Finish the greedy head: block best -> global atomic max -> last block
+// publishes the token, bumps the position and clears the sync words.
+__device__ __forceinline__ void argmax_finish(const GemvArgs& a, uint64_t best, uint64_t* keys) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) keys[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = keys[0];
+    for (int i = 1; i < kBlock / kWave; ++i) b = keys[i] > b ? keys[i] : b;
+    if (b != 0) atomicMax(reinterpret_cast<unsigned long long*>(a.slot), b);
+    __threadfence();
+    const unsigned done = atomicAdd(a.counter, 1u);
+    if (done == gridDim.x - 1) {
+      __threadfence();
+      const uint64_t k = atomicExch(reinterpret_cast<unsigned long long*>(a.slot), 0ull);
+      a.token_out[0] = static_cast<int64_t>(argmax_key_index(k));
+      if (a.position_inc) a.position_inc[0] += 1;
+      atomicExch(a.counter, 0u);
+    }
+  }
+}
+
+template <int R, int S, int U, bool NORM, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
+  float* red = reinterpret_cast<float*>(smem + 64);
+  bf16_t* xs = reinterpret_cast<bf16_t*>(smem + kLdsHead);
+  stage_x<NORM>(a, xs, red);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kv = a.k >> 3;
+  const int chunks = (kv + 63) >> 6;
+  const long groups = (a.n + R - 1) / R;
+  uint64_t best = 0;
+
+  for (long grp = static_cast<long>(blockIdx.x) * 4 + wave; grp < groups;
+       grp += static_cast<long>(gridDim.x) * 4) {
+    const long n0 = grp * R;
+    const bf16_t* rows[R][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const long n = n0 + r < a.n ? n0 + r : a.n - 1;
+#pragma unroll
+      for (int s = 0; s < S; ++s) rows[r][s] = a.w + (n + s * a.n) * static_cast<long>(a.k);
+    }
+    float acc[R][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int s = 0; s < S; ++s) acc[r][s] = 0.f;
+
+    for (int c0 = 0; c0 < chunks; c0 += U) {
+      uint4 wv[U][R][S];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = (c0 + u) * 64 + lane;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            wv[u][r][s] = v < kv ? load_stream(rows[r][s] + v * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (c0 + u < chunks) {
+          const int v = (c0 + u) * 64 + lane;
+          float xf[8];
+          unpack8(*reinterpret_cast<const uint4*>(xs + v * 8), xf);
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[r][s] += dot8(wv[u][r][s], xf);
+        }
+      }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const long n = n0 + r;
+      float t0 = wave_sum(acc[r][0]);
+      float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
+      if (n < a.n) {
+        if (EPI == EPI_ARGMAX) {
+          const uint64_t key = argmax_key(f2bf(t0), static_cast<uint32_t>(n));
+          best = key > best ? key : best;
+        } else if (lane == 0) {
+          float out;
+          if (EPI == EPI_STORE) {
+            out = t0;
+          } else if (EPI == EPI_RESIDUAL) {
+            out = round_bf(t0) + bf2f(a.res[n]);
+          } else {
+            out = silu_mul(round_bf(t0), round_bf(t1));
+          }
+          a.y[n] = static_cast<bf16_t>(f2bf(out));
+        }
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) argmax_finish(a, best, keys);
+}
+
+// Generic fallback for row lengths that are not a multiple of 8 or unaligned
+// pointers: scalar loads, one wave per row. Same epilogues and rounding.
+template <bool NORM, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_scalar(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
+  float* red = reinterpret_cast<float*>(smem + 64);
+  float* xs = reinterpret_cast<float*>(smem + kLdsHead);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float ss = 0.f;
+  for (int i = tid; i < a.k; i += kBlock) {
+    const float f = bf2f(a.x[i]);
+    xs[i] = f;
+    ss = fmaf(f, f, ss);
+  }
+  if (NORM) {
+    const float total = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(a.k) + a.eps);
+    for (int i = tid; i < a.k; i += kBlock) xs[i] = round_bf(bf2f(a.gain[i]) * round_bf(xs[i] * inv));
+  }
+  __syncthreads();
+  uint64_t best = 0;
+  const int S = EPI == EPI_SWIGLU ? 2 : 1;
+  for (long n = static_cast<long>(blockIdx.x) * 4 + wave; n < a.n; n += static_cast<long>(gridDim.x) * 4) {
+    float acc0 = 0.f, acc1 = 0.f;
+    const bf16_t* r0 = a.w + n * static_cast<long>(a.k);
+    const bf16_t* r1 = a.w + (n + a.n) * static_cast<long>(a.k);
+    for (int i = lane; i < a.k; i += kWave) {
+      acc0 = fmaf(bf2f(r0[i]), xs[i], acc0);
+      if (S > 1) acc1 = fmaf(bf2f(r1[i]), xs[i], acc1);
+    }
+    const float t0 = wave_sum(acc0);
+    const float t1 = wave_sum(acc1);
+    if (EPI == EPI_ARGMAX) {
+      const uint64_t key = argmax_key(f2bf(t0), static_cast<uint32_t>(n));
+      best = key > best ? key : best;
+    } else if (lane == 0) {
+      float out;
+      if (EPI == EPI_STORE) out = t0;
+      else if (EPI == EPI_RESIDUAL) out = round_bf(t0) + bf2f(a.res[n]);
+      else out = silu_mul(round_bf(t0), round_bf(t1));
+      a.y[n] = static_cast<bf16_t>(f2bf(out));
+    }
+  }
+  if (EPI == EPI_ARGMAX) argmax_finish(a, best, keys);
+}
+
+// Row-wise argmax over materialised bf16 logits: one block per row.
+__global__ __launch_bounds__(kBlock) void argmax_rows(const bf16_t* logits, long n, int64_t* out) {
+  __shared__ uint64_t keys[4];
+  const long row = blockIdx.x;
+  const bf16_t* p = logits + row * n;
+  uint64_t best = 0;
+  for (long i = threadIdx.x; i < n; i += kBlock) {
+    const uint64_t key = argmax_key(p[i], static_cast<uint32_t>(i));
+    best = key > best ? key : best;
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) keys[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = keys[0];
+    for (int i = 1; i < 4; ++i) b = keys[i] > b ? keys[i] : b;
+    out[row] = static_cast<int64_t>(argmax_key_index(b));
+  }
+}
+
+// ------------------------------------------------------------------ host dispatch
+
+namespace {
+
+constexpr int kMaxK = 16384;
+
+template <int R, int S, int U, bool NORM, int EPI>
+int launch_vec(const GemvArgs& a, hipStream_t st) {
+  const long groups = (a.n + R - 1) / R;
+  long blocks = (groups + 3) / 4;
+  const long cap = static_cast<long>(device_cus()) * 8;
+  if (EPI == EPI_ARGMAX) {
+    // One atomic per block; keep the grid to a few blocks per CU.
+    const long c2 = static_cast<long>(device_cus()) * 4;
+    blocks = blocks < c2 ? blocks : c2;
+  }
+  blocks = blocks < cap ? blocks : cap;
+  if (blocks < 1) blocks = 1;
+  const size_t lds = static_cast<size_t>(a.kpad) * 2 + kLdsHead;
+  hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
+  return launch_status();
+}
+
+template <bool NORM, int EPI>
+int launch_scalar(const GemvArgs& a, hipStream_t st) {
+  long blocks = (a.n + 3) / 4;
+  const long cap = static_cast<long>(device_cus()) * 4;
+  blocks = blocks < cap ? blocks : cap;
+  const size_t lds = static_cast<size_t>(a.k) * 4 + kLdsHead;
+  hipLaunchKernelGGL((gemv_scalar<NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
+  return launch_status();
+}
+
+// Loads in flight per lane = U * R * S; aim for ~16 (64 VGPRs of weights).
+template <bool NORM, int EPI>
+int dispatch(GemvArgs& a, hipStream_t st) {
+  const bool vec = (a.k % 8 == 0) && aligned16(a.x) && aligned16(a.w) &&
+                   (!NORM || aligned16(a.gain));
+  if (!vec) return launch_scalar<NORM, EPI>(a, st);
+  a.kpad = (a.k + 511) / 512 * 512;
+  const int chunks = a.kpad / 512;
+  constexpr int S = EPI == EPI_SWIGLU ? 2 : 1;
+  if (chunks <= 2) return launch_vec<(S == 2 ? 4 : 8), S, 2, NORM, EPI>(a, st);
+  if (chunks <= 6) return launch_vec<(S == 2 ? 2 : 4), S, 4, NORM, EPI>(a, st);
+  return launch_vec<(S == 2 ? 1 : 2), S, 8, NORM, EPI>(a, st);
+}
+
+bool bad_sizes(int64_t n, int64_t k) { return n <= 0 || k <= 0 || k > kMaxK || n > (1L << 31); }
+
+}  // namespace
+}  // namespace htn
+
+using namespace htn;
+
+extern "C" int htn_gemv(const void* x, const void* w, void* y, int64_t rows, int64_t k,
+                        htn_stream_t stream) {
+  if (!x || !w || !y || bad_sizes(rows, k)) return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  return dispatch<false, EPI_STORE>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int htn_gemv_norm(const void* x, const void* gain, float eps, const void* w,
+                             void* y, int64_t rows, int64_t k, int swiglu,
+                             htn_stream_t stream) {
+  if (!x || !gain || !w || !y || bad_sizes(rows, k)) return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.gain = static_cast<const bf16_t*>(gain);
+  a.w = static_cast<const bf16_t*>(w);
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return swiglu ? dispatch<true, EPI_SWIGLU>(a, st) : dispatch<true, EPI_STORE>(a, st);
+}
+
+extern "C" int htn_gemv_residual(const void* x, const void* w, const void* residual, void* y,
+                                 int64_t rows, int64_t k, htn_stream_t stream) {
+  if (!x || !w || !residual || !y || bad_sizes(rows, k)) return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.res = static_cast<const bf16_t*>(residual);
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  return dispatch<false, EPI_RESIDUAL>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
+                                  int64_t vocab, int64_t k, int64_t* token_out,
+                                  int64_t* position_inc, void* sync, htn_stream_t stream) {
+  if (!x || !w || !token_out || !sync || bad_sizes(vocab, k)) return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.gain = static_cast<const bf16_t*>(gain);
+  a.w = static_cast<const bf16_t*>(w);
+  a.n = vocab;
+  a.k = static_cast<int>(k);
+  a.eps = eps;
+  a.token_out = token_out;
+  a.position_inc = position_inc;
+  a.slot = static_cast<uint64_t*>(sync);
+  a.counter = reinterpret_cast<unsigned*>(static_cast<char*>(sync) + 8);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return gain ? dispatch<true, EPI_ARGMAX>(a, st) : dispatch<false, EPI_ARGMAX>(a, st);
+}
+
+extern "C" int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
+                               htn_stream_t stream) {
+  if (!logits || !out || rows <= 0 || n <= 0 || rows > (1L << 31) || n > (1L << 31))
+    return HTN_EINVAL;
+  hipLaunchKernelGGL(argmax_rows, dim3(rows), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16_t*>(logits), static_cast<long>(n), out);
+  return launch_status();
+}

@@ -1,0 +1,276 @@
+// Row-wise kernels: RMSNorm, residual-add + RMSNorm, SwiGLU, embedding gather.
+//
+// All four are pure HBM streams (no reuse), so the layout is one wave per row
+// with 16-byte loads and stores, four rows per 256-thread block, and a
+// wave64 DPP reduction for the sum of squares. Rows whose width or pointers
+// do not allow 16-byte access take a scalar path with identical rounding.
+#include "common.h"
+
+namespace htn {
+
+// Shared RMSNorm body: v holds the fp32 row values this lane owns.
+//   out = bf16(gain * bf16(v * inv)), inv = 1 / sqrt(sum(v^2) / cols + eps)
+// The division and square root are correctly rounded, as in torch's CPU rsqrt.
+__device__ __forceinline__ float rms_inv(float ss, int cols, float eps) {
+  return 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(cols) + eps);
+}
+
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void norm_rows_vec(const bf16_t* __restrict__ x, long x_stride,
+                                                        const bf16_t* __restrict__ r,
+                                                        const bf16_t* __restrict__ gain,
+                                                        bf16_t* __restrict__ summed,
+                                                        bf16_t* __restrict__ out, long rows,
+                                                        int cols, float eps) {
+  constexpr int kMaxVec = 16;  // up to 8192 columns per row
+  const int lane = threadIdx.x & 63;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wave exits together
+  const int nv = cols >> 3;
+  uint4 vals[kMaxVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int v = j * 64 + lane;
+    vals[j] = make_uint4(0, 0, 0, 0);
+    if (v < nv) {
+      uint4 xv = *reinterpret_cast<const uint4*>(x + row * x_stride + v * 8);
+      if (ADD) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(r + row * static_cast<long>(cols) + v * 8);
+        xv.x = pack_bf2(bf_lo(xv.x) + bf_lo(rv.x), bf_hi(xv.x) + bf_hi(rv.x));
+        xv.y = pack_bf2(bf_lo(xv.y) + bf_lo(rv.y), bf_hi(xv.y) + bf_hi(rv.y));
+        xv.z = pack_bf2(bf_lo(xv.z) + bf_lo(rv.z), bf_hi(xv.z) + bf_hi(rv.z));
+        xv.w = pack_bf2(bf_lo(xv.w) + bf_lo(rv.w), bf_hi(xv.w) + bf_hi(rv.w));
+        *reinterpret_cast<uint4*>(summed + row * static_cast<long>(cols) + v * 8) = xv;
+      }
+      vals[j] = xv;
+      float f[8];
+      unpack8(xv, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+  }
+  const float inv = rms_inv(ss, cols, eps);
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int v = j * 64 + lane;
+    if (v < nv) {
+      float f[8], g[8];
+      unpack8(vals[j], f);
+      unpack8(*reinterpret_cast<const uint4*>(gain + v * 8), g);
+      uint4 o;
+      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+      *reinterpret_cast<uint4*>(out + row * static_cast<long>(cols) + v * 8) = o;
+    }
+  }
+}
+
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void norm_rows_scalar(const bf16_t* __restrict__ x, long x_stride,
+                                                           const bf16_t* __restrict__ r,
+                                                           const bf16_t* __restrict__ gain,
+                                                           bf16_t* __restrict__ summed,
+                                                           bf16_t* __restrict__ out, long rows,
+                                                           int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float ss = 0.f;
+  for (int c = lane; c < cols; c += kWave) {
+    float f = bf2f(x[row * x_stride + c]);
+    if (ADD) {
+      const uint32_t s = f2bf(f + bf2f(r[row * cols + c]));
+      summed[row * cols + c] = static_cast<bf16_t>(s);
+      f = bf2f(s);
+    }
+    ss = fmaf(f, f, ss);
+  }
+  const float inv = rms_inv(ss, cols, eps);
+  for (int c = lane; c < cols; c += kWave) {
+    const float f = ADD ? bf2f(summed[row * cols + c]) : bf2f(x[row * x_stride + c]);
+    out[row * cols + c] = static_cast<bf16_t>(f2bf(bf2f(gain[c]) * round_bf(f * inv)));
+  }
+}
+
+// out = bf16(bf16(silu(g)) * u), one thread per 8 columns.
+__global__ __launch_bounds__(kBlock) void swiglu_vec(const bf16_t* __restrict__ g, long gs,
+                                                     const bf16_t* __restrict__ u, long us,
+                                                     bf16_t* __restrict__ out, long rows, int cols) {
+  const int nv = cols >> 3;
+  const long total = rows * nv;
+  for (long i = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<long>(gridDim.x) * kBlock) {
+    const long row = i / nv;
+    const int v = static_cast<int>(i - row * nv);
+    float gf[8], uf[8];
+    unpack8(*reinterpret_cast<const uint4*>(g + row * gs + v * 8), gf);
+    unpack8(*reinterpret_cast<const uint4*>(u + row * us + v * 8), uf);
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float sig = 1.0f / (1.0f + expf(-gf[k]));
+      o[k] = round_bf(gf[k] * sig) * uf[k];
+    }
+    uint4 w;
+    w.x = pack_bf2(o[0], o[1]);
+    w.y = pack_bf2(o[2], o[3]);
+    w.z = pack_bf2(o[4], o[5]);
+    w.w = pack_bf2(o[6], o[7]);
+    *reinterpret_cast<uint4*>(out + row * cols + v * 8) = w;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_scalar(const bf16_t* __restrict__ g, long gs,
+                                                        const bf16_t* __restrict__ u, long us,
+                                                        bf16_t* __restrict__ out, long rows, int cols) {
+  const long total = rows * cols;
+  for (long i = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<long>(gridDim.x) * kBlock) {
+    const long row = i / cols;
+    const int c = static_cast<int>(i - row * cols);
+    const float gf = bf2f(g[row * gs + c]);
+    const float sig = 1.0f / (1.0f + expf(-gf));
+    out[i] = static_cast<bf16_t>(f2bf(round_bf(gf * sig) * bf2f(u[row * us + c])));
+  }
+}
+
+// One block per token id; 16-byte copies of the embedding row.
+__global__ __launch_bounds__(kBlock) void embed_vec(const int64_t* __restrict__ ids,
+                                                    const bf16_t* __restrict__ table, long vocab,
+                                                    int hidden, bf16_t* __restrict__ out) {
+  const long t = blockIdx.x;
+  const int64_t id = ids[t];
+  const bool ok = id >= 0 && id < vocab;
+  const int nv = hidden >> 3;
+  for (int v = threadIdx.x; v < nv; v += kBlock) {
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (ok) val = *reinterpret_cast<const uint4*>(table + id * hidden + v * 8);
+    *reinterpret_cast<uint4*>(out + t * hidden + v * 8) = val;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void embed_scalar(const int64_t* __restrict__ ids,
+                                                       const bf16_t* __restrict__ table, long vocab,
+                                                       int hidden, bf16_t* __restrict__ out) {
+  const long t = blockIdx.x;
+  const int64_t id = ids[t];
+  const bool ok = id >= 0 && id < vocab;
+  for (int c = threadIdx.x; c < hidden; c += kBlock)
+    out[t * hidden + c] = ok ? table[id * hidden + c] : static_cast<bf16_t>(0);
+}
+
+namespace {
+int g_cus[64];
+}
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
+}
+
+}  // namespace htn
+
+using namespace htn;
+
+extern "C" int htn_version(void) { return 1; }
+
+namespace {
+
+int norm_launch(bool add, const void* x, int64_t x_stride, const void* r, const void* gain,
+                void* summed, void* out, int64_t rows, int64_t cols, float eps,
+                htn_stream_t stream) {
+  if (!x || !gain || !out || rows <= 0 || cols <= 0 || cols > 8192 || x_stride < cols)
+    return HTN_EINVAL;
+  if (add && (!r || !summed)) return HTN_EINVAL;
+  const bool vec = cols % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(gain) &&
+                   aligned16(out) && (!add || (aligned16(r) && aligned16(summed)));
+  const dim3 grid((rows + 3) / 4);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t* xp = static_cast<const bf16_t*>(x);
+  const bf16_t* rp = static_cast<const bf16_t*>(r);
+  const bf16_t* gp = static_cast<const bf16_t*>(gain);
+  bf16_t* sp = static_cast<bf16_t*>(summed);
+  bf16_t* op = static_cast<bf16_t*>(out);
+  if (vec) {
+    if (add)
+      hipLaunchKernelGGL(norm_rows_vec<true>, grid, dim3(kBlock), 0, st, xp, x_stride, rp, gp, sp, op,
+                         rows, static_cast<int>(cols), eps);
+    else
+      hipLaunchKernelGGL(norm_rows_vec<false>, grid, dim3(kBlock), 0, st, xp, x_stride, rp, gp, sp,
+                         op, rows, static_cast<int>(cols), eps);
+  } else {
+    if (add)
+      hipLaunchKernelGGL(norm_rows_scalar<true>, grid, dim3(kBlock), 0, st, xp, x_stride, rp, gp, sp,
+                         op, rows, static_cast<int>(cols), eps);
+    else
+      hipLaunchKernelGGL(norm_rows_scalar<false>, grid, dim3(kBlock), 0, st, xp, x_stride, rp, gp,
+                         sp, op, rows, static_cast<int>(cols), eps);
+  }
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" int htn_rms_norm(const void* x, int64_t x_row_stride, const void* gain, void* out,
+                            int64_t rows, int64_t cols, float eps, htn_stream_t stream) {
+  return norm_launch(false, x, x_row_stride, nullptr, gain, nullptr, out, rows, cols, eps, stream);
+}
+
+extern "C" int htn_add_rms_norm(const void* x, const void* residual, const void* gain,
+                                void* summed, void* normalized, int64_t rows, int64_t cols,
+                                float eps, htn_stream_t stream) {
+  return norm_launch(true, x, cols, residual, gain, summed, normalized, rows, cols, eps, stream);
+}
+
+extern "C" int htn_swiglu(const void* gate, int64_t gate_row_stride, const void* up,
+                          int64_t up_row_stride, void* out, int64_t rows, int64_t cols,
+                          htn_stream_t stream) {
+  if (!gate || !up || !out || rows <= 0 || cols <= 0 || gate_row_stride < cols ||
+      up_row_stride < cols)
+    return HTN_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = cols % 8 == 0 && gate_row_stride % 8 == 0 && up_row_stride % 8 == 0 &&
+                   aligned16(gate) && aligned16(up) && aligned16(out);
+  const long work = vec ? rows * (cols / 8) : rows * cols;
+  long blocks = (work + kBlock - 1) / kBlock;
+  const long cap = static_cast<long>(device_cus()) * 16;
+  blocks = blocks < cap ? blocks : cap;
+  if (vec)
+    hipLaunchKernelGGL(swiglu_vec, dim3(blocks), dim3(kBlock), 0, st, static_cast<const bf16_t*>(gate),
+                       static_cast<long>(gate_row_stride), static_cast<const bf16_t*>(up),
+                       static_cast<long>(up_row_stride), static_cast<bf16_t*>(out),
+                       static_cast<long>(rows), static_cast<int>(cols));
+  else
+    hipLaunchKernelGGL(swiglu_scalar, dim3(blocks), dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(gate), static_cast<long>(gate_row_stride),
+                       static_cast<const bf16_t*>(up), static_cast<long>(up_row_stride),
+                       static_cast<bf16_t*>(out), static_cast<long>(rows), static_cast<int>(cols));
+  return launch_status();
+}
+
+extern "C" int htn_embed_gather(const int64_t* ids, int64_t count, const void* table,
+                                int64_t vocab, int64_t hidden, void* out, htn_stream_t stream) {
+  if (!ids || !table || !out || count <= 0 || vocab <= 0 || hidden <= 0 || count > (1L << 31))
+    return HTN_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = hidden % 8 == 0 && aligned16(table) && aligned16(out);
+  if (vec)
+    hipLaunchKernelGGL(embed_vec, dim3(count), dim3(kBlock), 0, st, ids,
+                       static_cast<const bf16_t*>(table), static_cast<long>(vocab),
+                       static_cast<int>(hidden), static_cast<bf16_t*>(out));
+  else
+    hipLaunchKernelGGL(embed_scalar, dim3(count), dim3(kBlock), 0, st, ids,
+                       static_cast<const bf16_t*>(table), static_cast<long>(vocab),
+                       static_cast<int>(hidden), static_cast<bf16_t*>(out));
+  return launch_status();
+}

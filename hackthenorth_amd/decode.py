@@ -1,0 +1,255 @@
+"""Fixed-address KV storage and a graph-captured single-token decode step.
+
+Mirrors dryft/engine/decode.py: KVCache (25-46), RotaryTable (49-67),
+forward (78-99), DecodeState (102-206) and stream_decode (8-22), with the
+same device-resident token/position state so a captured step replays
+without host involvement. The batch-one step is five HIP kernels per layer:
+
+  gemv_norm(ln1, W_qkv) -> decode attention (QK-norm, RoPE from the table at
+  the device position, KV append, split-KV softmax and merge) ->
+  gemv_residual(W_o) -> gemv_norm_swiglu(ln2, W_gate_up) -> gemv_residual(W_down)
+
+plus one embedding gather before the layers and one fused
+final-norm/LM-head/argmax kernel after them, which also writes the token and
+advances the position.
+"""
+import torch
+
+from .kernels.attention import decode_attention, grouped_attention
+from .kernels.down import down_residual
+from .kernels.embed import embed_gather
+from .kernels.fused import norm_rope_cache
+from .kernels.greedy import greedy_head
+from .kernels.projection import norm_projection, output_projection_residual
+from .speculate import draft_width, verified_tokens
+
+
+def stream_decode(state, first_tokens, output_length):
+    """Launch the next step before yielding the current tokens (decode.py:8-22).
+
+    Only the Python list crosses the yield; output_length=1 launches nothing.
+    """
+    tokens = first_tokens
+    for step in range(output_length):
+        has_next = step + 1 < output_length
+        if has_next:
+            state.graph.replay()
+        yield tokens
+        if has_next:
+            tokens = state.token[:, 0].tolist()
+
+
+class KVCache:
+    """Per-layer K and V of shape [B, Hkv, capacity, 128], zero-filled, in one allocation."""
+
+    def __init__(self, model, batch_size, capacity):
+        c = model.config
+        shape = (c.num_hidden_layers, 2, batch_size, c.num_key_value_heads, capacity, c.head_dim)
+        # Masked slots must still be finite: the zero fill keeps them so.
+        self.storage = torch.zeros(shape, dtype=model.dtype, device=model.device)
+        self.keys = [self.storage[i, 0] for i in range(c.num_hidden_layers)]
+        self.values = [self.storage[i, 1] for i in range(c.num_hidden_layers)]
+        self.capacity = capacity
+        self.prefill = True
+
+
+def rope_tables(config, capacity):
+    """Default RoPE rows for positions 0..capacity-1, computed like the model's
+    rotary module (fp32 inverse frequencies and angles, cos/sin rounded to bf16)."""
+    d = config.head_dim
+    inv_freq = 1.0 / (config.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+    angles = torch.arange(capacity, dtype=torch.int64).float()[:, None] * inv_freq[None, :]
+    emb = torch.cat((angles, angles), dim=-1)
+    return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+
+class RotaryTable:
+    """Prompt-independent RoPE rows for every cache slot, resident on the device.
+
+    `tables` is (cos, sin), each [1, capacity, 128], as the reference's table
+    (decode.py:55-62); `select` gathers rows by device positions. The decode
+    step reads the row for the device position inside the attention kernel.
+    """
+
+    def __init__(self, model, capacity, enabled=True):
+        cos, sin = rope_tables(model.config, capacity)
+        self.tables = (cos[None].to(model.device), sin[None].to(model.device))
+
+    def select(self, positions):
+        return tuple(t.index_select(1, positions) for t in self.tables)
+
+
+def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=None, record=None):
+    """Batch-one single-token step through the fused kernels.
+
+    `record`, when a list, receives the hidden state after every layer."""
+    c = model.config
+    groups = c.num_attention_heads // c.num_key_value_heads
+    q_width, k_width, _ = c.widths
+    cos, sin = rotary.tables
+    h = embed_gather(token_ids.reshape(1), model.embed_weight)
+    for i, layer in enumerate(model.layers):
+        ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+        packed = norm_projection(h, ln1.weight, layer.qkv_weight, ln1.variance_epsilon)
+        a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
+                             cache.keys[i], cache.values[i], position,
+                             c.num_key_value_heads, groups, q_width, q_width + k_width)
+        r = output_projection_residual(a, layer.o_weight, h)
+        m = norm_projection(r, ln2.weight, layer.gate_up_weight, ln2.variance_epsilon,
+                            swiglu=True)
+        h = down_residual(m, layer.down_weight, r)
+        if record is not None:
+            record.append(h)
+    if out is None:
+        out = torch.empty((1, 1), dtype=torch.int64, device=model.device)
+    greedy_head(h, model.norm.weight, model.norm.variance_epsilon, model.lm_head_weight,
+                out, advance)
+    return out
+
+
+def _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings, rotary):
+    """Any batch and token count: per-row GEMVs, batched norm/RoPE/cache and attention."""
+    c = model.config
+    b, t = token_ids.shape
+    hidden = c.hidden_size
+    if position_embeddings is None:
+        position_embeddings = rotary.select(positions)
+    cos, sin = position_embeddings
+    h = embed_gather(token_ids, model.embed_weight).reshape(b * t, hidden)
+    widths = c.widths
+    for i, layer in enumerate(model.layers):
+        ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+        packed = torch.stack([norm_projection(h[r], ln1.weight, layer.qkv_weight,
+                                              ln1.variance_epsilon) for r in range(b * t)])
+        q, k, v = packed.view(b, t, -1).split(widths, -1)
+        shape = (b, t, -1, c.head_dim)
+        q, _, _ = norm_rope_cache(q.view(shape), k.view(shape), v.view(shape), layer.q_norm,
+                                  layer.k_norm, cos, sin, cache.keys[i], cache.values[i],
+                                  positions)
+        a = grouped_attention(q, cache.keys[i], cache.values[i], positions)
+        a = a.transpose(1, 2).reshape(b * t, -1).contiguous()
+        r = torch.stack([output_projection_residual(a[j], layer.o_weight, h[j])
+                         for j in range(b * t)])
+        m = torch.stack([norm_projection(r[j], ln2.weight, layer.gate_up_weight,
+                                         ln2.variance_epsilon, swiglu=True)
+                         for j in range(b * t)])
+        h = torch.stack([down_residual(m[j], layer.down_weight, r[j]) for j in range(b * t)])
+    h = h.view(b, t, hidden)
+    x = h[:, -1:] if last_only else h
+    rows = x.reshape(-1, hidden).contiguous()
+    out = torch.empty((rows.shape[0],), dtype=torch.int64, device=model.device)
+    for r in range(rows.shape[0]):
+        greedy_head(rows[r], model.norm.weight, model.norm.variance_epsilon,
+                    model.lm_head_weight, out[r:r + 1])
+    return out.view(b, x.shape[1])
+
+
+def forward(model, token_ids, cache, positions, attention_mask=None, last_only=True,
+            position_embeddings=None, *, rotary=None, out=None, advance=None, record=None):
+    """Greedy next tokens [B, 1] (or [B, T] with last_only=False) (decode.py:78-99).
+
+    Causality comes from the absolute `positions` (device int64, one per
+    token) inside the attention kernels, so `attention_mask` is accepted and
+    ignored, as in the reference's position-causal attention. K/V of the new
+    tokens are written to cache slots `positions`. With a RotaryTable and a
+    single token at batch one the fused step runs; `out`/`advance` then
+    receive the token and a position increment in place, and `record` (a
+    list) collects the per-layer hidden states.
+    """
+    b, t = token_ids.shape
+    if b == 1 and t == 1 and rotary is not None and position_embeddings is None:
+        return _decode_one(model, token_ids, cache, positions, rotary, out, advance, record)
+    if rotary is None and position_embeddings is None:
+        rotary = RotaryTable(model, cache.capacity)
+    tokens = _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings,
+                           rotary)
+    if out is not None:
+        out.copy_(tokens[:, -1:])
+    if advance is not None:
+        advance.add_(t)
+    return tokens
+
+
+class DecodeState:
+    """Cache, rotary table, device token/position and the captured step (decode.py:102-206)."""
+
+    def __init__(self, model, batch_size, prompt_length, output_length, speculative=False,
+                 cache_rotary=True, omit_unused_masks=True):
+        self.shape = (batch_size, prompt_length, output_length)
+        self.draft_tokens = draft_width(output_length) if speculative and batch_size == 1 else 0
+        # Tail verification may write beyond the last requested output; causal
+        # attention hides those scratch slots from earlier queries.
+        capacity = prompt_length + output_length - 1 + self.draft_tokens
+        device = model.device
+        self.model = model
+        self.capacity = capacity
+        self.cache = KVCache(model, batch_size, capacity)
+        self.prompt_positions = torch.arange(prompt_length, device=device)
+        self.token = torch.zeros((batch_size, 1), dtype=torch.int64, device=device)
+        self.position = torch.full((1,), prompt_length, dtype=torch.int64, device=device)
+        self.rotary = RotaryTable(model, capacity, enabled=cache_rotary)
+        self.graph = None
+        self.verify_graph = None
+        if output_length > 1:
+            self.capture(model)
+
+    def step(self, model):
+        forward(model, self.token, self.cache, self.position, rotary=self.rotary,
+                out=self.token, advance=self.position)
+
+    def capture(self, model):
+        self.cache.prefill = False
+        prompt_length = self.shape[1]
+        stream = torch.cuda.Stream(device=model.device)
+        stream.wait_stream(torch.cuda.current_stream(model.device))
+        with torch.cuda.stream(stream):
+            # Library load, sync buffer and allocator warm-up happen off capture.
+            for _ in range(2):
+                self.position.fill_(prompt_length)
+                self.step(model)
+            self.position.fill_(prompt_length)
+        torch.cuda.current_stream(model.device).wait_stream(stream)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=stream):
+            self.step(model)
+
+    def prefill(self, model, input_ids):
+        """Run the prompt through the decode step one token at a time.
+
+        Each replay attends over the slots written so far, which is the causal
+        prefill computed token by token; afterwards `token` holds the greedy
+        continuation and `position` equals the prompt length.
+        """
+        batch, length = input_ids.shape
+        if (batch, length) != self.shape[:2]:
+            raise ValueError("prompt shape differs from the state's shape")
+        self.cache.prefill = False
+        self.position.fill_(0)
+        if batch == 1:
+            for i in range(length):
+                self.token.copy_(input_ids[:, i:i + 1])
+                if self.graph is not None:
+                    self.graph.replay()
+                else:
+                    self.step(model)
+        else:
+            token = forward(model, input_ids, self.cache, self.prompt_positions,
+                            rotary=self.rotary)
+            self.token.copy_(token)
+            self.position.fill_(length)
+        return self.token
+
+    def verify(self, current_token, proposal, position):
+        """Score [current, *proposal] at positions position.. in one pass and keep
+        the verified prefix plus one target token (decode.py:197-206)."""
+        inputs = torch.tensor([[current_token, *proposal]], dtype=torch.int64,
+                              device=self.token.device)
+        positions = torch.arange(position, position + inputs.shape[1], device=self.token.device)
+        predictions = forward(self.model, inputs, self.cache, positions, last_only=False,
+                              rotary=self.rotary)
+        emitted = verified_tokens(proposal, predictions[0].tolist())
+        self.token.copy_(predictions[:, len(emitted) - 1:len(emitted)])
+        # The speculative tail is discarded logically: later queries mask it and
+        # later steps overwrite those slots.
+        self.position.fill_(position + len(emitted))
+        return emitted

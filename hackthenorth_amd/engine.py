@@ -1,0 +1,62 @@
+"""Engine(model_path).generate(input_ids, max_new_tokens) (dryft/engine/engine.py:175-249).
+
+Contract (QWEN_ENGINE_CONTRACT.md:24-36 in the reference): generate yields
+one list with one token id per sequence for every output step, exactly
+max_new_tokens times, greedy, never stopping at end-of-sequence ids.
+"""
+import torch
+
+from .decode import DecodeState, stream_decode
+from .model import Qwen3Model
+from .speculate import BackoffPromptLookup
+
+
+class Engine:
+    def __init__(self, model_path: str, speculative: bool = True, device="cuda") -> None:
+        """Load config.json (+ safetensors, or the seeded random init) onto the GPU.
+
+        speculative=False disables the batch-one prompt-lookup verifier, giving
+        one decode step per output token.
+        """
+        if not torch.cuda.is_available():
+            raise RuntimeError("Engine needs a HIP GPU")
+        self.model = Qwen3Model.from_pretrained(model_path, device)
+        self.speculative = speculative
+        self.state = None
+
+    def generate(self, input_ids: list, max_new_tokens: int):
+        if max_new_tokens <= 0:
+            return
+        with torch.inference_mode():
+            shape = (len(input_ids), len(input_ids[0]), max_new_tokens)
+            if self.state is None or self.state.shape != shape:
+                self.state = None
+                self.state = DecodeState(self.model, *shape, speculative=self.speculative)
+            state = self.state
+            prompt = torch.tensor(input_ids, dtype=torch.int64, device=self.model.device)
+            current = state.prefill(self.model, prompt)
+            tokens = current[:, 0].tolist()
+            if state.draft_tokens == 0:
+                yield from stream_decode(state, tokens, max_new_tokens)
+                return
+            yield tokens
+            lookup = BackoffPromptLookup(input_ids[0], draft_length=state.draft_tokens)
+            lookup.append(tokens[0])
+            emitted = 1
+            while emitted < max_new_tokens:
+                proposal = lookup.propose()
+                if proposal:
+                    verified = state.verify(tokens[0], proposal, shape[1] + emitted - 1)
+                    # Scratch slots let a verify run at any position; emit only
+                    # what the request still owes.
+                    for token in verified[:max_new_tokens - emitted]:
+                        tokens = [token]
+                        lookup.append(token)
+                        emitted += 1
+                        yield tokens
+                else:
+                    state.graph.replay()
+                    tokens = state.token[:, 0].tolist()
+                    lookup.append(tokens[0])
+                    emitted += 1
+                    yield tokens

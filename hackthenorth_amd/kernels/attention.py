@@ -1,0 +1,93 @@
+"""Grouped-query decode attention over fixed KV storage (dryft/engine/kernels/attention.py).
+
+Q is [B, Hq, Q, 128]; K/V are contiguous [B, Hkv, capacity, 128]; positions
+holds one absolute cache position per query (int64, on device). Query t sees
+slots <= positions[t]; slots after the largest position are never read.
+Output has Q's shape, contiguous bf16. Inputs are not mutated (the prologue
+variant appends the newest k/v to the cache, as the reference's does).
+"""
+import torch
+
+from .. import _lib
+
+
+def _scratch(device, batch, heads, queries, capacity):
+    nbytes = _lib.load().htn_attention_scratch_bytes(batch, heads, queries, capacity)
+    return torch.empty((max(nbytes, 4) + 3) // 4, dtype=torch.float32, device=device)
+
+
+def _check_cache(keys, values, batch, kv_heads):
+    if keys.shape != values.shape or keys.dim() != 4 or keys.shape[0] != batch \
+            or keys.shape[1] != kv_heads or keys.shape[3] != _lib.HEAD_DIM \
+            or not keys.is_contiguous() or not values.is_contiguous() \
+            or keys.dtype != torch.bfloat16 or values.dtype != torch.bfloat16:
+        raise ValueError("caches must be contiguous bf16 [B, Hkv, capacity, 128]")
+
+
+def grouped_attention(q, k, v, positions):
+    """softmax(q k^T / sqrt(128)) v per query over its visible slots (attention.py:213-237)."""
+    batch, heads, queries, dim = q.shape
+    kv_heads = k.shape[1]
+    if dim != _lib.HEAD_DIM or q.stride(-1) != 1 or q.dtype != torch.bfloat16:
+        raise ValueError("q must be bf16 [B, Hq, Q, 128] with unit dim stride")
+    if heads % kv_heads:
+        raise ValueError("query heads must be a multiple of kv heads")
+    _check_cache(k, v, batch, kv_heads)
+    if positions.dtype != torch.int64 or positions.numel() != queries:
+        raise ValueError("positions must be int64 with one entry per query")
+    _lib.require_gpu(q, k, v, positions)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    scratch = _scratch(q.device, batch, heads, queries, k.shape[2])
+    _lib.call("htn_grouped_attention", _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2),
+              _lib.ptr(k), _lib.ptr(v), k.shape[2], _lib.ptr(positions.contiguous()),
+              _lib.ptr(out), batch, heads, kv_heads, queries, _lib.ptr(scratch),
+              _lib.ptr(_lib.sync_buffer(q.device)), _lib.stream(q.device))
+    return out
+
+
+def _prologue(qkv, q_norm, k_norm, cos, sin, by_position, keys, values, positions, kv_heads,
+              groups, k_offset, v_offset):
+    batch, width = qkv.shape[0], qkv.shape[-1]
+    if qkv.numel() != batch * width or qkv.stride(-1) != 1 or qkv.dtype != torch.bfloat16:
+        raise ValueError("qkv must be a bf16 [B, 1, width] packed projection")
+    if cos.shape != sin.shape or cos.shape[-1] != _lib.HEAD_DIM or not cos.is_contiguous() \
+            or not sin.is_contiguous():
+        raise ValueError("cos/sin must be contiguous 128-wide rows")
+    _check_cache(keys, values, batch, kv_heads)
+    heads = kv_heads * groups
+    if k_offset < heads * _lib.HEAD_DIM or v_offset < k_offset + kv_heads * _lib.HEAD_DIM \
+            or v_offset + kv_heads * _lib.HEAD_DIM > width:
+        raise ValueError("k/v offsets do not fit the packed projection")
+    if positions.dtype != torch.int64:
+        raise ValueError("positions must be int64")
+    _lib.require_gpu(qkv, keys, values, positions, cos, sin)
+    rope_rows = cos.numel() // _lib.HEAD_DIM
+    out = torch.empty((batch, heads, 1, _lib.HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
+    scratch = _scratch(qkv.device, batch, heads, 1, keys.shape[2])
+    _lib.call("htn_prologue_attention", _lib.ptr(qkv), qkv.stride(0), k_offset, v_offset,
+              _lib.ptr(q_norm.weight), _lib.ptr(k_norm.weight), float(q_norm.variance_epsilon),
+              float(k_norm.variance_epsilon), _lib.ptr(cos), _lib.ptr(sin), _lib.HEAD_DIM,
+              rope_rows, int(by_position), _lib.ptr(keys), _lib.ptr(values), keys.shape[2],
+              _lib.ptr(positions), _lib.ptr(out), batch, kv_heads, groups, _lib.ptr(scratch),
+              _lib.ptr(_lib.sync_buffer(qkv.device)), _lib.stream(qkv.device))
+    return out
+
+
+def prologue_attention(qkv, q_norm, k_norm, cos, sin, keys, values, positions,
+                       kv_heads, groups, k_offset, v_offset):
+    """Single-token decode attention with norm/rope/cache-write fused in (attention.py:162).
+
+    qkv is the packed (batch, 1, width) projection; cos/sin the selected
+    [1, 1, 128] rows. Writes the newest K/V into slot positions[0] and
+    returns [batch, heads, 1, 128].
+    """
+    return _prologue(qkv, q_norm, k_norm, cos, sin, False, keys, values, positions, kv_heads,
+                     groups, k_offset, v_offset)
+
+
+def decode_attention(qkv, q_norm, k_norm, cos_table, sin_table, keys, values, position,
+                     kv_heads, groups, k_offset, v_offset):
+    """prologue_attention reading the RoPE row for position[0] straight from the
+    [capacity, 128] tables, so the decode step needs no index_select launch."""
+    return _prologue(qkv, q_norm, k_norm, cos_table, sin_table, True, keys, values, position,
+                     kv_heads, groups, k_offset, v_offset)

@@ -1,0 +1,175 @@
+/* htn_decode.h -- C ABI of the MI355X (gfx950) batch-one Qwen3 decode kernels.
+ *
+ * Every entry point takes raw device pointers, explicit sizes/strides and a
+ * HIP stream (passed as void*), launches asynchronously on that stream and
+ * returns HTN_OK or a negative error code. No entry point allocates device
+ * memory, synchronises the host or reads device data on the host, so all of
+ * them may be captured into a HIP graph.
+ *
+ * bf16 tensors are raw 16-bit patterns. Unless a stride is given, tensors are
+ * contiguous row-major. Positions and token ids are int64 device arrays that
+ * the kernels read on the device (graph replays see updated values).
+ *
+ * "sync" buffers are caller-owned, zero-initialised device buffers of
+ * HTN_SYNC_BYTES bytes holding completion counters; kernels leave them zero
+ * again when they finish, so one buffer serves every call made in stream
+ * order. Calls that run concurrently on one sync buffer race.
+ *
+ * Reference interfaces cited as file:line are in rickytang666/hackthenorth,
+ * under dryft/engine/.
+ */
+#ifndef HTN_DECODE_H
+#define HTN_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HTN_OK 0
+#define HTN_EINVAL (-1)       /* bad pointer, size, stride or alignment */
+#define HTN_EUNSUPPORTED (-2) /* shape the kernels do not implement */
+#define HTN_ELAUNCH (-3)      /* the HIP launch failed */
+
+#define HTN_SYNC_BYTES 4096
+#define HTN_HEAD_DIM 128
+
+typedef void* htn_stream_t;
+
+/* Library version, for the loader's sanity check. */
+int htn_version(void);
+
+/* ---------------------------------------------------------------- weights */
+
+/* out[i] = bf16(f32(IrwinHall4(hash(seed, stream, start + i)) - 131070) * scale),
+ * i < count. Bit-identical to the numpy generator used by the tests.
+ * Replaces the reference's torch RNG initialisation of random weights. */
+int htn_fill_normal_bf16(void* out, int64_t count, uint64_t seed, uint64_t stream,
+                         int64_t start, float scale, htn_stream_t stream_);
+
+/* out[i] = floor((hash >> 32) * high / 2^32) as int64. */
+int htn_fill_randint_i64(int64_t* out, int64_t count, uint64_t seed, uint64_t stream,
+                         int64_t high, htn_stream_t stream_);
+
+/* ---------------------------------------------------------------- gather */
+
+/* out[t, :] = table[ids[t], :] for t < count (bf16 rows of `hidden`).
+ * Ids outside [0, vocab) produce a zero row instead of an out-of-bounds read.
+ * Replaces base.embed_tokens(token_ids), decode.py:81. */
+int htn_embed_gather(const int64_t* ids, int64_t count, const void* table, int64_t vocab,
+                     int64_t hidden, void* out, htn_stream_t stream);
+
+/* ---------------------------------------------------------------- norms */
+
+/* out = bf16(gain * bf16(x * rsqrt(mean(x^2) + eps))) per row.
+ * Replaces rms_norm(x, weight, eps), kernels/rmsnorm.py:84. */
+int htn_rms_norm(const void* x, int64_t x_row_stride, const void* gain, void* out,
+                 int64_t rows, int64_t cols, float eps, htn_stream_t stream);
+
+/* summed = bf16(x + residual); normalized = rms_norm(summed).
+ * Replaces add_rms_norm(x, residual, weight, eps), kernels/rmsnorm.py:35. */
+int htn_add_rms_norm(const void* x, const void* residual, const void* gain, void* summed,
+                     void* normalized, int64_t rows, int64_t cols, float eps,
+                     htn_stream_t stream);
+
+/* out[r, c] = bf16(bf16(silu(gate[r, c])) * up[r, c]); out contiguous.
+ * Replaces swiglu(gate, up), kernels/fused.py:171. */
+int htn_swiglu(const void* gate, int64_t gate_row_stride, const void* up,
+               int64_t up_row_stride, void* out, int64_t rows, int64_t cols,
+               htn_stream_t stream);
+
+/* ---------------------------------------------------------------- batch-one GEMV */
+
+/* y[n] = bf16(sum_k x[k] * w[n, k]) for n < rows; w is [rows, k] row-major. */
+int htn_gemv(const void* x, const void* w, void* y, int64_t rows, int64_t k,
+             htn_stream_t stream);
+
+/* RMSNorm prologue then projection: y = W . bf16(gain * bf16(x * inv)).
+ * swiglu != 0: w holds gate rows [0, rows) then up rows [rows, 2 rows) and
+ * y[n] = bf16(bf16(silu(bf16 gate_n)) * bf16 up_n).
+ * Replaces norm_projection(x, gain, weight, eps, swiglu=...),
+ * kernels/projection.py:36. */
+int htn_gemv_norm(const void* x, const void* gain, float eps, const void* w, void* y,
+                  int64_t rows, int64_t k, int swiglu, htn_stream_t stream);
+
+/* y[n] = bf16(bf16(sum_k x[k] w[n, k]) + residual[n]).
+ * Replaces output_projection_residual(x, weight, residual),
+ * kernels/projection.py:70, and down_residual(x, w, residual),
+ * kernels/down.py:27 (same rounding: projection rounded before the add). */
+int htn_gemv_residual(const void* x, const void* w, const void* residual, void* y,
+                      int64_t rows, int64_t k, htn_stream_t stream);
+
+/* Greedy head: token = argmax_n bf16(W[n] . xn) with the lowest id on ties,
+ * where xn = x, or rms_norm(x, gain, eps) when gain is not NULL (the final
+ * norm fused in). Writes token_out[0]; when position_inc is not NULL it also
+ * adds 1 to position_inc[0] after every block has read it (the decode step's
+ * position.add_(1)). `sync` is an HTN_SYNC_BYTES buffer.
+ * Replaces greedy_token(x, w), kernels/greedy.py:45, and
+ * lm_head(x).argmax(-1), decode.py:96-99. */
+int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
+                       int64_t vocab, int64_t k, int64_t* token_out,
+                       int64_t* position_inc, void* sync, htn_stream_t stream);
+
+/* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
+int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
+                    htn_stream_t stream);
+
+/* ---------------------------------------------------------------- attention (D = 128) */
+
+/* Per-head RMSNorm + RoPE of q and k, for tokens t < T of batch b < B:
+ *   q[b, t, h, :] at q + b*q_sb + t*q_st + h*128 (likewise k, v);
+ *   cos/sin row for token t at cos + rope_row(t)*rope_st, where
+ *   rope_row(t) = positions[t] if rope_by_position else t; rows at or past
+ *   rope_rows (the table length) are skipped, never read.
+ * out_q is [B, T, Hq, 128] contiguous. When keys/values are not NULL the
+ * normalised k and the raw v are written to cache slot positions[t] of the
+ * [B, Hkv, cap, 128] caches; when out_k is not NULL the normalised k is also
+ * written to out_k [B, T, Hkv, 128]. positions may be NULL when it is not
+ * needed (no cache write and rope_by_position == 0).
+ * Replaces norm_rope_cache(...), kernels/fused.py:70, and
+ * norm_rope(...), kernels/fused.py:132. */
+int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k,
+                        int64_t k_sb, int64_t k_st, const void* v, int64_t v_sb,
+                        int64_t v_st, const void* q_gain, const void* k_gain, float q_eps,
+                        float k_eps, const void* cos, const void* sin, int64_t rope_st,
+                        int64_t rope_rows, int rope_by_position, void* keys, void* values,
+                        int64_t cap,
+                        const int64_t* positions, void* out_q, void* out_k, int64_t B,
+                        int64_t T, int64_t Hq, int64_t Hkv, htn_stream_t stream);
+
+/* Bytes of fp32 scratch the attention entry points need for these sizes. */
+int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap);
+
+/* Grouped-query attention over fixed-capacity caches with causality by
+ * absolute position: query t of head h sees slots <= positions[t] of kv head
+ * h / (Hq / Hkv); later slots are never read. q[b, h, t, :] at
+ * q + b*q_sb + h*q_sh + t*q_st; out is [B, Hq, Q, 128] contiguous.
+ * Split-KV with the merge done by the last block of each kv head.
+ * Replaces grouped_attention(q, k, v, positions), kernels/attention.py:213. */
+int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                          const void* keys, const void* values, int64_t cap,
+                          const int64_t* positions, void* out, int64_t B, int64_t Hq,
+                          int64_t Hkv, int64_t Q, void* scratch, void* sync,
+                          htn_stream_t stream);
+
+/* Single-token decode attention with the QK-norm/RoPE/cache append fused in:
+ * q, the newest k and v come from the packed projection row
+ * qkv[b, :] (row stride qkv_sb; k at k_off, v at v_off). The cos/sin row is
+ * cos + rope_row*rope_st with rope_row = positions[0] if rope_by_position
+ * else 0. Writes the newest k/v into slot positions[0] and returns
+ * out [B, Hq, 128].
+ * Replaces prologue_attention(...), kernels/attention.py:162. */
+int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off,
+                           const void* q_gain, const void* k_gain, float q_eps, float k_eps,
+                           const void* cos, const void* sin, int64_t rope_st,
+                           int64_t rope_rows, int rope_by_position, void* keys, void* values,
+                           int64_t cap,
+                           const int64_t* positions, void* out, int64_t B, int64_t Hkv,
+                           int64_t groups, void* scratch, void* sync, htn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HTN_DECODE_H */

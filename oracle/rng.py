@@ -1,0 +1,122 @@
+"""Counter-based RNG restated in numpy -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this package, and only as the checker of the HIP library: nothing in the
+product path imports it.
+
+The generator is a splitmix64 finaliser applied to (key + (i+1) * golden)
+where key mixes a 64-bit seed and a 64-bit stream id. Every step is integer
+arithmetic or a single correctly rounded fp32 multiply followed by
+round-to-nearest-even to bfloat16, so the HIP generator in
+hackthenorth_amd/csrc/rng.hip produces bit-identical tensors on any machine.
+The reference draws its test tensors from torch's RNG
+(dryft/tests/test_fused_kernels.py:21-37); torch streams are not stable across
+machines, so the shapes and distributions are kept and the generator replaced.
+
+Distributions:
+  normal(std)   Irwin-Hall sum of four 16-bit uniforms, centred and scaled to
+                unit variance (|z| <= 3.46), times std -- an approximation of
+                N(0, std^2) that stays bit-reproducible.
+  randint(n)    multiply-shift of the top 32 bits: floor(u32 * n / 2^32).
+  uniform(a,b)  a + (b-a) * (top 24 bits / 2^24), fp32 multiply then add.
+
+Parity pinned: tests/test_oracle_rng.py checks the moments, the range
+limits, and hand-computed splitmix64 values for known counters.
+"""
+import numpy as np
+
+GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+STREAM_MUL = np.uint64(0xD1B54A32D192ED03)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+# Irwin-Hall(4) over 16-bit uniforms: mean 4*65535/2, variance 4*(65536^2-1)/12.
+IH_MEAN = 131070
+IH_STD = float(np.sqrt(4.0 * (65536.0 ** 2 - 1.0) / 12.0))
+
+CHUNK = 1 << 22
+
+
+def mix64(z):
+    """splitmix64 finaliser on uint64 arrays (wrap-around arithmetic)."""
+    z = np.asarray(z, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+    return z ^ (z >> np.uint64(31))
+
+
+def stream_key(seed, stream):
+    with np.errstate(over="ignore"):
+        return mix64(np.uint64(seed) ^ (np.uint64(stream) * STREAM_MUL))
+
+
+def hashes(seed, stream, start, count):
+    """64-bit hash of counters start..start+count-1 for (seed, stream)."""
+    key = stream_key(seed, stream)
+    idx = np.arange(start + 1, start + count + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        return mix64(key + idx * GOLDEN)
+
+
+def normal_scale(std):
+    """fp32 multiplier applied to the centred Irwin-Hall integer."""
+    return np.float32(std / IH_STD)
+
+
+def f32_to_bf16_bits(x):
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16); NaN stays NaN."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    with np.errstate(over="ignore"):
+        r = u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))
+    out = (r >> np.uint32(16)).astype(np.uint16)
+    out[nan] = ((u[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
+    return out
+
+
+def bf16_bits_to_f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def normal_f32(seed, stream, count, std=1.0, start=0):
+    """fp32 values before the bf16 rounding (exact products, see module doc)."""
+    out = np.empty(count, dtype=np.float32)
+    scale = normal_scale(std)
+    for lo in range(0, count, CHUNK):
+        n = min(CHUNK, count - lo)
+        h = hashes(seed, stream, start + lo, n)
+        m = np.uint64(0xFFFF)
+        s = ((h & m) + ((h >> np.uint64(16)) & m) + ((h >> np.uint64(32)) & m)
+             + (h >> np.uint64(48))).astype(np.int64) - IH_MEAN
+        out[lo:lo + n] = s.astype(np.float32) * scale
+    return out
+
+
+def normal_bf16_bits(seed, stream, count, std=1.0, start=0):
+    out = np.empty(count, dtype=np.uint16)
+    for lo in range(0, count, CHUNK):
+        n = min(CHUNK, count - lo)
+        out[lo:lo + n] = f32_to_bf16_bits(normal_f32(seed, stream, n, std, start + lo))
+    return out
+
+
+def randint(seed, stream, count, high, start=0):
+    """Uniform integers in [0, high) as int64."""
+    h = hashes(seed, stream, start, count)
+    with np.errstate(over="ignore"):
+        return (((h >> np.uint64(32)) * np.uint64(high)) >> np.uint64(32)).astype(np.int64)
+
+
+def uniform_f32(seed, stream, count, low, high, start=0):
+    h = hashes(seed, stream, start, count)
+    u = (h >> np.uint64(40)).astype(np.float32) * np.float32(1.0 / (1 << 24))
+    return np.float32(low) + np.float32(high - low) * u
+
+
+def int8_uniform(seed, stream, count, start=0):
+    """Uniform int8 in [-127, 127]."""
+    h = hashes(seed, stream, start, count)
+    with np.errstate(over="ignore"):
+        v = ((h >> np.uint64(32)) * np.uint64(255)) >> np.uint64(32)
+    return (v.astype(np.int64) - 127).astype(np.int8)

@@ -1,0 +1,39 @@
+"""The C-ABI library loads on the host and exports every entry point the header declares."""
+import ctypes
+import os
+import re
+
+from hackthenorth_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "htn_decode.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(?:int|int64_t)\s+(htn_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    names = declared()
+    assert names, "no entry points parsed from the header"
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.htn_version() == 1
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    # Null pointers and bad sizes are rejected before any launch.
+    assert lib.htn_gemv(null, null, null, 16, 16, null) == _lib.HTN_EINVAL
+    assert lib.htn_rms_norm(null, 16, null, null, 1, 16, 1e-6, null) == _lib.HTN_EINVAL
+    assert lib.htn_embed_gather(None, 1, null, 10, 8, null, null) == _lib.HTN_EINVAL
+    assert lib.htn_attention_scratch_bytes(1, 16, 1, 575) > 0
+    assert lib.htn_attention_scratch_bytes(0, 16, 1, 575) == 0
