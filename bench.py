@@ -145,6 +145,7 @@ def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
                       f"({prefill_s:.1f}s) then {decode_steps} greedy decode steps at ctx "
                       f"{len(prompt)}-{len(prompt) + decode_steps - 1}; tok/s over the decode steps",
             "prefill_s": round(prefill_s, 3), "tokens_match_gpu": bool(agree),
+            "cpu_tokens": tokens, "gpu_tokens": [first_gpu] + list(steps_gpu_tokens[:decode_steps]),
             "cpu_model": cpu_name, "os_cpu_count": os.cpu_count(),
             "affinity_cpus": len(os.sched_getaffinity(0))}
 

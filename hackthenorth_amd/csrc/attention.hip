@@ -23,7 +23,9 @@ constexpr int D = HTN_HEAD_DIM;
 constexpr int kRowChunk = 8;        // query rows held in registers at once
 constexpr int kMaxRows = 32;        // G * Q
 constexpr int kSyncAttnOffset = 64; // attention counters start here in the sync buffer
-constexpr int kSlotUnroll = 4;      // 16-slot passes issued back to back
+constexpr int kSlotUnroll = 4;      // 16-slot groups per wave: 64 slots per block pass
+constexpr int kMaxSplit = 16 * kSlotUnroll;
+constexpr int kMergeUnroll = 8;     // partials loaded back to back in the merge
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
 //   n = bf16(g * bf16(x * inv)); out_i = bf16(bf16(n_i cos_i) + bf16(rot(n)_i sin_i)).
@@ -115,15 +117,16 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int rows = a.G * a.Q;
   float* qs = reinterpret_cast<float*>(smem);                     // [rows][D]
-  float* sc = qs + rows * D;                                      // [rows][split]
-  float* accr = sc + rows * a.split;                              // [4][kRowChunk][D]
-  float* mrow = accr + 4 * kRowChunk * D;                         // [rows]
-  float* lrow = mrow + kMaxRows;                                  // [rows]
+  float* sc = qs + rows * D;                                      // [rows][kMaxSplit]
+  float* accr = sc + rows * kMaxSplit;                            // [4][kRowChunk][D]
+  float* mrow = accr + 4 * kRowChunk * D;                         // [kMaxRows]
+  float* lrow = mrow + kMaxRows;                                  // [kMaxRows]
   bf16_t* knew = reinterpret_cast<bf16_t*>(lrow + kMaxRows);      // [D]
   bf16_t* vnew = knew + D;                                        // [D]
   int* flag = reinterpret_cast<int*>(vnew + D);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane >> 4, e = lane & 15;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
 
@@ -136,7 +139,22 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   const bool active = start <= maxpos;
   const int64_t newest = FUSED ? a.pos[0] : -1;
 
-  // ---- query rows (and, fused, the newest k/v) into LDS
+  // ---- 1. issue this block's K and V loads first: they depend only on the
+  // positions, so their HBM latency overlaps the query prologue. Lane (sub, e)
+  // of wave w owns slot start + u*16 + w*4 + sub, dims e*8 .. e*8+7.
+  uint4 kreg[kSlotUnroll], vreg[kSlotUnroll];
+#pragma unroll
+  for (int u = 0; u < kSlotUnroll; ++u) {
+    const long j = start + u * 16 + wave * 4 + sub;
+    kreg[u] = make_uint4(0, 0, 0, 0);
+    vreg[u] = make_uint4(0, 0, 0, 0);
+    if (active && j < end && !(FUSED && j == newest)) {
+      kreg[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
+      vreg[u] = *reinterpret_cast<const uint4*>(a.values + kv_base + j * D + e * 8);
+    }
+  }
+
+  // ---- 2. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
     const long rr = a.rope_by_pos ? newest : 0;
     const bool rope_ok = rr >= 0 && rr < a.rope_rows;
@@ -153,15 +171,17 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       float o0, o1;
       norm_rope_wave(row + a.k_off + static_cast<long>(kvh) * D, a.kg, a.k_eps, cs, sn, lane, o0, o1);
       const bf16_t* vsrc = row + a.v_off + static_cast<long>(kvh) * D;
-      knew[lane] = static_cast<bf16_t>(f2bf(o0));
-      knew[lane + 64] = static_cast<bf16_t>(f2bf(o1));
-      vnew[lane] = vsrc[lane];
-      vnew[lane + 64] = vsrc[lane + 64];
+      const bf16_t k0 = static_cast<bf16_t>(f2bf(o0)), k1 = static_cast<bf16_t>(f2bf(o1));
+      const bf16_t v0 = vsrc[lane], v1 = vsrc[lane + 64];
+      knew[lane] = k0;
+      knew[lane + 64] = k1;
+      vnew[lane] = v0;
+      vnew[lane + 64] = v1;
       const long slot = kv_base + newest * D;
-      a.keys[slot + lane] = knew[lane];
-      a.keys[slot + lane + 64] = knew[lane + 64];
-      a.values[slot + lane] = vsrc[lane];
-      a.values[slot + lane + 64] = vsrc[lane + 64];
+      a.keys[slot + lane] = k0;
+      a.keys[slot + lane + 64] = k1;
+      a.values[slot + lane] = v0;
+      a.values[slot + lane + 64] = v1;
     }
   } else {
     for (int i = tid; i < rows * D; i += kBlock) {
@@ -173,11 +193,18 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  const int sub = lane >> 4, e = lane & 15;
   const int len = active ? static_cast<int>(end - start) : 0;
-
   if (active) {
-    // ---- scores: each 16-lane row of a wave owns one cache slot
+    if (FUSED && newest >= start && newest < end) {
+#pragma unroll
+      for (int u = 0; u < kSlotUnroll; ++u) {
+        if (start + u * 16 + wave * 4 + sub == newest) {
+          kreg[u] = *reinterpret_cast<const uint4*>(knew + e * 8);
+          vreg[u] = *reinterpret_cast<const uint4*>(vnew + e * 8);
+        }
+      }
+    }
+    // ---- 3. scores q.k * D^-1/2 into LDS (16 lanes per slot, DPP row sums)
     for (int r0 = 0; r0 < rows; r0 += kRowChunk) {
       const int nr = rows - r0 < kRowChunk ? rows - r0 : kRowChunk;
       float qr[kRowChunk][8];
@@ -185,32 +212,17 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       for (int r = 0; r < kRowChunk; ++r)
 #pragma unroll
         for (int i = 0; i < 8; ++i) qr[r][i] = r < nr ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
-      // kSlotUnroll passes of 16 slots per iteration keep several loads in flight per lane.
-      for (long j0 = start + wave * 4; j0 < end; j0 += 16 * kSlotUnroll) {
-        uint4 kv[kSlotUnroll];
 #pragma unroll
-        for (int u = 0; u < kSlotUnroll; ++u) {
-          const long j = j0 + u * 16 + sub;
-          kv[u] = make_uint4(0, 0, 0, 0);
-          if (j < end) {
-            if (FUSED && j == newest)
-              kv[u] = *reinterpret_cast<const uint4*>(knew + e * 8);
-            else
-              kv[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
-          }
-        }
+      for (int u = 0; u < kSlotUnroll; ++u) {
+        const long j = start + u * 16 + wave * 4 + sub;
 #pragma unroll
-        for (int u = 0; u < kSlotUnroll; ++u) {
-          const long j = j0 + u * 16 + sub;
-#pragma unroll
-          for (int r = 0; r < kRowChunk; ++r) {
-            if (r < nr) {
-              const float dsum = row16_sum(dot8(kv[u], qr[r]));
-              if (e == 0 && j < end) {
-                const int rr = r0 + r;
-                const int64_t qpos = a.pos[rr % a.Q];
-                sc[rr * a.split + (j - start)] = j <= qpos ? dsum * a.scale : -INFINITY;
-              }
+        for (int r = 0; r < kRowChunk; ++r) {
+          if (r < nr) {
+            const float dsum = row16_sum(dot8(kreg[u], qr[r]));
+            if (e == 0 && j < end) {
+              const int rr = r0 + r;
+              const int64_t qpos = a.pos[rr % a.Q];
+              sc[rr * kMaxSplit + (j - start)] = j <= qpos ? dsum * a.scale : -INFINITY;
             }
           }
         }
@@ -218,18 +230,13 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- exact softmax numerators per row
+    // ---- 4. exact softmax numerators per row (the split's own max)
     for (int r = wave; r < rows; r += 4) {
-      float m = -INFINITY;
-      for (int i = lane; i < len; i += kWave) m = fmaxf(m, sc[r * a.split + i]);
-      m = wave_max(m);
-      float l = 0.f;
-      for (int i = lane; i < len; i += kWave) {
-        const float p = m == -INFINITY ? 0.f : expf(sc[r * a.split + i] - m);
-        sc[r * a.split + i] = p;
-        l += p;
-      }
-      l = wave_sum(l);
+      const float v = lane < len ? sc[r * kMaxSplit + lane] : -INFINITY;
+      const float m = wave_max(v);
+      const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
+      if (lane < len) sc[r * kMaxSplit + lane] = p;
+      const float l = wave_sum(p);
       if (lane == 0) {
         mrow[r] = m;
         lrow[r] = l;
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- P.V, partial per row
+    // ---- 5. P.V from the V rows already in registers
     for (int r0 = 0; r0 < rows; r0 += kRowChunk) {
       const int nr = rows - r0 < kRowChunk ? rows - r0 : kRowChunk;
       float acc[kRowChunk][8];
@@ -245,32 +252,18 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       for (int r = 0; r < kRowChunk; ++r)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[r][i] = 0.f;
-      for (long j0 = start + wave * 4; j0 < end; j0 += 16 * kSlotUnroll) {
-        uint4 vv[kSlotUnroll];
 #pragma unroll
-        for (int u = 0; u < kSlotUnroll; ++u) {
-          const long j = j0 + u * 16 + sub;
-          vv[u] = make_uint4(0, 0, 0, 0);
-          if (j < end) {
-            if (FUSED && j == newest)
-              vv[u] = *reinterpret_cast<const uint4*>(vnew + e * 8);
-            else
-              vv[u] = *reinterpret_cast<const uint4*>(a.values + kv_base + j * D + e * 8);
-          }
-        }
+      for (int u = 0; u < kSlotUnroll; ++u) {
+        const long j = start + u * 16 + wave * 4 + sub;
+        if (j < end) {
+          float vf[8];
+          unpack8(vreg[u], vf);
 #pragma unroll
-        for (int u = 0; u < kSlotUnroll; ++u) {
-          const long j = j0 + u * 16 + sub;
-          if (j < end) {
-            float vf[8];
-            unpack8(vv[u], vf);
+          for (int r = 0; r < kRowChunk; ++r) {
+            if (r < nr) {
+              const float p = sc[(r0 + r) * kMaxSplit + (j - start)];
 #pragma unroll
-            for (int r = 0; r < kRowChunk; ++r) {
-              if (r < nr) {
-                const float p = sc[(r0 + r) * a.split + (j - start)];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[r][i] = fmaf(p, vf[i], acc[r][i]);
-              }
+              for (int i = 0; i < 8; ++i) acc[r][i] = fmaf(p, vf[i], acc[r][i]);
             }
           }
         }
@@ -313,7 +306,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
 
   if (a.splits == 1) return;
 
-  // ---- the last block of this kv head merges the partials
+  // ---- 6. the last block of this kv head merges the partials
   __threadfence();
   __syncthreads();
   if (tid == 0) {
@@ -325,6 +318,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   __threadfence();
   const int nact = static_cast<int>(maxpos / a.split) + 1 < a.splits
                        ? static_cast<int>(maxpos / a.split) + 1 : a.splits;
+  // (a) per row: global max M and denominator L over the active splits
   for (int r = wave; r < rows; r += 4) {
     const int h = kvh * a.G + r / a.Q, t = r % a.Q;
     const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
@@ -343,38 +337,59 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  for (int i = tid; i < rows * D; i += kBlock) {
-    const int r = i / D, d = i % D;
+  // (b) out = sum_s exp(m_s - M) acc_s / L, 4 dims per thread, loads unrolled
+  for (int i = tid; i < rows * (D / 4); i += kBlock) {
+    const int r = i / (D / 4), d4 = (i % (D / 4)) * 4;
     const int h = kvh * a.G + r / a.Q, t = r % a.Q;
     const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
     const float m = mrow[r];
-    float v = 0.f;
-    for (int sp = 0; sp < nact; ++sp) {
-      const float mi = a.ml[(orow * a.splits + sp) * 2];
-      if (mi != -INFINITY) v = fmaf(expf(mi - m), a.part[(orow * a.splits + sp) * D + d], v);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nact; s0 += kMergeUnroll) {
+      float4 pv[kMergeUnroll];
+      float mv[kMergeUnroll];
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        const int sp = s0 + u < nact ? s0 + u : nact - 1;
+        pv[u] = *reinterpret_cast<const float4*>(a.part + (orow * a.splits + sp) * D + d4);
+        mv[u] = a.ml[(orow * a.splits + sp) * 2];
+      }
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        const float w = (s0 + u < nact && mv[u] != -INFINITY) ? expf(mv[u] - m) : 0.f;
+        v.x = fmaf(w, pv[u].x, v.x);
+        v.y = fmaf(w, pv[u].y, v.y);
+        v.z = fmaf(w, pv[u].z, v.z);
+        v.w = fmaf(w, pv[u].w, v.w);
+      }
     }
-    a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrow[r]));
+    const float l = lrow[r];
+    bf16_t* o = a.out + orow * D + d4;
+    o[0] = static_cast<bf16_t>(f2bf(v.x / l));
+    o[1] = static_cast<bf16_t>(f2bf(v.y / l));
+    o[2] = static_cast<bf16_t>(f2bf(v.z / l));
+    o[3] = static_cast<bf16_t>(f2bf(v.w / l));
   }
   if (tid == 0) a.counters[static_cast<long>(b) * a.Hkv + kvh] = 0u;
 }
 
 // Split size: about two blocks per CU over (batch, kv head, split), slices of
-// 16..256 cache slots (16 = one pass of four slots per wave).
+// 32..64 cache slots (a 64-slot slice is one register-resident pass: four
+// 16-slot groups per wave).
 void choose_split(long B, long Hkv, long rows, long cap, int* split, int* splits) {
   const long target = 2L * device_cus();
   long per_head = target / (B * Hkv);
   if (per_head < 1) per_head = 1;
-  long want = (cap + per_head - 1) / per_head;
-  long sz = 16;
-  while (sz < want) sz <<= 1;
-  const long max_split = rows > 16 ? 128 : 256;
-  if (sz > max_split) sz = max_split;
+  const long want = (cap + per_head - 1) / per_head;
+  long sz = 32;
+  while (sz < want && sz < kMaxSplit) sz <<= 1;
+  (void)rows;
   *split = static_cast<int>(sz);
   *splits = static_cast<int>((cap + sz - 1) / sz);
 }
 
 size_t attention_lds(int rows, int split) {
-  return static_cast<size_t>(rows) * D * 4 + static_cast<size_t>(rows) * split * 4 +
+  (void)split;
+  return static_cast<size_t>(rows) * D * 4 + static_cast<size_t>(rows) * kMaxSplit * 4 +
          4 * kRowChunk * D * 4 + 2 * kMaxRows * 4 + 2 * D * 2 + 16;
 }
 
@@ -411,7 +426,7 @@ extern "C" int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q,
   // Worst case over kv-head counts dividing Hq: the split grows with Hkv * B.
   int split = 0, splits = 0;
   choose_split(B, 1, Hq * Q, cap, &split, &splits);
-  int split_min = 16;
+  int split_min = 32;
   const long most = (cap + split_min - 1) / split_min;
   const long n = static_cast<long>(B) * Hq * Q * (most > splits ? most : splits);
   return n * (D + 2) * 4;

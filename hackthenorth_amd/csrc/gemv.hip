@@ -103,30 +103,49 @@ __device__ __forceinline__ void argmax_finish(const GemvArgs& a, uint64_t best, 
   }
 }
 
+template <int R, int S, int U>
+__device__ __forceinline__ void issue_batch(const GemvArgs& a, long grp, int c0, int kv, int lane,
+                                            uint4 (&wv)[U][R][S]) {
+  const long n0 = grp * R;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long n = n0 + r < a.n ? n0 + r : a.n - 1;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const bf16_t* row = a.w + (n + s * a.n) * static_cast<long>(a.k);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = (c0 + u) * 64 + lane;
+        wv[u][r][s] = v < kv ? load_stream(row + v * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+}
+
 template <int R, int S, int U, bool NORM, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
   float* red = reinterpret_cast<float*>(smem + 64);
   bf16_t* xs = reinterpret_cast<bf16_t*>(smem + kLdsHead);
-  stage_x<NORM>(a, xs, red);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kv = a.k >> 3;
   const int chunks = (kv + 63) >> 6;
   const long groups = (a.n + R - 1) / R;
-  uint64_t best = 0;
+  const long stride = static_cast<long>(gridDim.x) * 4;
+  long grp = static_cast<long>(blockIdx.x) * 4 + wave;
 
-  for (long grp = static_cast<long>(blockIdx.x) * 4 + wave; grp < groups;
-       grp += static_cast<long>(gridDim.x) * 4) {
+  // The first weight batch does not depend on x: issue it before the
+  // activation/RMSNorm prologue so the two latencies overlap.
+  uint4 wv[U][R][S];
+  bool pending = grp < groups;
+  if (pending) issue_batch<R, S, U>(a, grp, 0, kv, lane, wv);
+  stage_x<NORM>(a, xs, red);
+
+  uint64_t best = 0;
+  for (; grp < groups; grp += stride) {
     const long n0 = grp * R;
-    const bf16_t* rows[R][S];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const long n = n0 + r < a.n ? n0 + r : a.n - 1;
-#pragma unroll
-      for (int s = 0; s < S; ++s) rows[r][s] = a.w + (n + s * a.n) * static_cast<long>(a.k);
-    }
     float acc[R][S];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -134,16 +153,8 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
       for (int s = 0; s < S; ++s) acc[r][s] = 0.f;
 
     for (int c0 = 0; c0 < chunks; c0 += U) {
-      uint4 wv[U][R][S];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int v = (c0 + u) * 64 + lane;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-            wv[u][r][s] = v < kv ? load_stream(rows[r][s] + v * 8) : make_uint4(0, 0, 0, 0);
-      }
+      if (!pending) issue_batch<R, S, U>(a, grp, c0, kv, lane, wv);
+      pending = false;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (c0 + u < chunks) {

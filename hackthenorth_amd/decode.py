@@ -79,25 +79,35 @@ class RotaryTable:
         return tuple(t.index_select(1, positions) for t in self.tables)
 
 
+def decode_layer(model, i, h, cache, position, rotary):
+    """Decoder layer i for one token at batch one: five kernels, h [1, H] -> [1, H].
+
+    Appends the layer's K/V at the device `position` and reads the RoPE row
+    for it from the rotary table inside the attention kernel.
+    """
+    c = model.config
+    layer = model.layers[i]
+    groups = c.num_attention_heads // c.num_key_value_heads
+    q_width, k_width, _ = c.widths
+    cos, sin = rotary.tables
+    ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+    packed = norm_projection(h, ln1.weight, layer.qkv_weight, ln1.variance_epsilon)
+    a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
+                         cache.keys[i], cache.values[i], position,
+                         c.num_key_value_heads, groups, q_width, q_width + k_width)
+    r = output_projection_residual(a, layer.o_weight, h)
+    m = norm_projection(r, ln2.weight, layer.gate_up_weight, ln2.variance_epsilon,
+                        swiglu=True)
+    return down_residual(m, layer.down_weight, r)
+
+
 def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=None, record=None):
     """Batch-one single-token step through the fused kernels.
 
     `record`, when a list, receives the hidden state after every layer."""
-    c = model.config
-    groups = c.num_attention_heads // c.num_key_value_heads
-    q_width, k_width, _ = c.widths
-    cos, sin = rotary.tables
     h = embed_gather(token_ids.reshape(1), model.embed_weight)
-    for i, layer in enumerate(model.layers):
-        ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
-        packed = norm_projection(h, ln1.weight, layer.qkv_weight, ln1.variance_epsilon)
-        a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
-                             cache.keys[i], cache.values[i], position,
-                             c.num_key_value_heads, groups, q_width, q_width + k_width)
-        r = output_projection_residual(a, layer.o_weight, h)
-        m = norm_projection(r, ln2.weight, layer.gate_up_weight, ln2.variance_epsilon,
-                            swiglu=True)
-        h = down_residual(m, layer.down_weight, r)
+    for i in range(len(model.layers)):
+        h = decode_layer(model, i, h, cache, position, rotary)
         if record is not None:
             record.append(h)
     if out is None:

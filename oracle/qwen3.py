@@ -228,6 +228,34 @@ class Oracle:
     def _linear(self, x, name):
         return (x.float() @ self.f32[name].T).to(BF16)
 
+    def layer(self, l, h, cache, positions):
+        """Decoder layer l on hidden rows h [B, T, H] at absolute `positions`.
+
+        Writes the layer's K/V for the new tokens into cache slots `positions`
+        (decode.py:35-46) and returns the layer output [B, T, H].
+        """
+        s = self.shape
+        w = self.weights
+        b, t = h.shape[:2]
+        d = s.head_dim
+        cos = self.cos[positions][None, :, None, :]      # [1, T, 1, D]
+        sin = self.sin[positions][None, :, None, :]
+        n = rms_norm(h, w[f"{l}.ln1"], s.eps)
+        qkv = self._linear(n, f"{l}.qkv")
+        q, k, v = qkv.split((s.q_heads * d, s.kv_heads * d, s.kv_heads * d), -1)
+        q = norm_rope(q.view(b, t, s.q_heads, d), w[f"{l}.q_norm"], cos, sin, s.eps)
+        k = norm_rope(k.view(b, t, s.kv_heads, d), w[f"{l}.k_norm"], cos, sin, s.eps)
+        v = v.reshape(b, t, s.kv_heads, d)
+        cache.keys[l][:, :, positions] = k.transpose(1, 2)
+        cache.values[l][:, :, positions] = v.transpose(1, 2)
+        a = attention(q.transpose(1, 2), cache.keys[l], cache.values[l], positions)
+        a = a.transpose(1, 2).reshape(b, t, s.q_heads * d)
+        r = (self._linear(a, f"{l}.o").float() + h.float()).to(BF16)
+        m = rms_norm(r, w[f"{l}.ln2"], s.eps)
+        gu = self._linear(m, f"{l}.gate_up")
+        act = silu_mul(gu[..., :s.ffn], gu[..., s.ffn:])
+        return (self._linear(act, f"{l}.down").float() + r.float()).to(BF16)
+
     def forward(self, ids, cache, positions, last_only=True, record=None):
         """ids [B, T] int64, positions [T] absolute; returns (tokens, logits_f32, logits_bf16).
 
@@ -236,27 +264,9 @@ class Oracle:
         """
         s = self.shape
         w = self.weights
-        b, t = ids.shape
-        d = s.head_dim
         h = w["embed"][ids]                              # [B, T, H]
-        cos = self.cos[positions][None, :, None, :]      # [1, T, 1, D]
-        sin = self.sin[positions][None, :, None, :]
         for l in range(s.layers):
-            n = rms_norm(h, w[f"{l}.ln1"], s.eps)
-            qkv = self._linear(n, f"{l}.qkv")
-            q, k, v = qkv.split((s.q_heads * d, s.kv_heads * d, s.kv_heads * d), -1)
-            q = norm_rope(q.view(b, t, s.q_heads, d), w[f"{l}.q_norm"], cos, sin, s.eps)
-            k = norm_rope(k.view(b, t, s.kv_heads, d), w[f"{l}.k_norm"], cos, sin, s.eps)
-            v = v.reshape(b, t, s.kv_heads, d)
-            cache.keys[l][:, :, positions] = k.transpose(1, 2)
-            cache.values[l][:, :, positions] = v.transpose(1, 2)
-            a = attention(q.transpose(1, 2), cache.keys[l], cache.values[l], positions)
-            a = a.transpose(1, 2).reshape(b, t, s.q_heads * d)
-            r = (self._linear(a, f"{l}.o").float() + h.float()).to(BF16)
-            m = rms_norm(r, w[f"{l}.ln2"], s.eps)
-            gu = self._linear(m, f"{l}.gate_up")
-            act = silu_mul(gu[..., :s.ffn], gu[..., s.ffn:])
-            h = (self._linear(act, f"{l}.down").float() + r.float()).to(BF16)
+            h = self.layer(l, h, cache, positions)
             if record is not None:
                 record.append(h.clone())
         x = rms_norm(h[:, -1:] if last_only else h, w["norm"], s.eps)
