@@ -77,9 +77,8 @@ def run_decode(shape, prompt_len, steps, warmup, log):
             state.graph.replay()
             tokens[i:i + 1].copy_(state.token[0])
         torch.cuda.synchronize()
-    weights = model.weight_bytes()
     mean_ctx = prompt_len + (steps - 1) / 2.0
-    bytes_per_token = weights + kv_bytes_per_token(cfg, mean_ctx)
+    bytes_per_token = model.decode_weight_bytes() + kv_bytes_per_token(cfg, mean_ctx)
     tok_s = steps / elapsed
     return dict(model=model, cfg=cfg, prompt=prompt.cpu().tolist(), first=int(first),
                 tokens=tokens.cpu().tolist(), elapsed=elapsed, tok_s=tok_s,
@@ -88,21 +87,31 @@ def run_decode(shape, prompt_len, steps, warmup, log):
 
 
 def dominant_kernel(model, launches=280):
-    """Fused norm + gate/up + SwiGLU GEMV over the layers' weights, HIP events on its stream."""
+    """Fused norm + gate/up + SwiGLU GEMV over the layers' weights (one launch per
+    layer, rotating through all of them), captured in a graph so the launches run
+    back to back, timed with HIP events on the capturing stream."""
     cfg = model.config
     layers = model.layers
     x = torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16, device=model.device)
     DR.normal_(x, 3, 99, 1.0)
     gain = layers[0].post_attention_layernorm.weight
-    for layer in layers[:4]:
-        P.norm_projection(x, gain, layer.gate_up_weight, 1e-6, swiglu=True)
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.Stream(device=model.device)
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for layer in layers[:4]:
+            P.norm_projection(x, gain, layer.gate_up_weight, 1e-6, swiglu=True)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(launches):
+            P.norm_projection(x, gain, layers[i % len(layers)].gate_up_weight, 1e-6, swiglu=True)
+    graph.replay()
     torch.cuda.synchronize()
-    start.record(stream)
-    for i in range(launches):
-        P.norm_projection(x, gain, layers[i % len(layers)].gate_up_weight, 1e-6, swiglu=True)
-    end.record(stream)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
     end.synchronize()
     avg_s = start.elapsed_time(end) / 1e3 / launches
     k, n2 = cfg.hidden_size, 2 * cfg.intermediate_size

@@ -18,7 +18,7 @@ HTN_OK = 0
 HTN_EINVAL = -1
 HTN_EUNSUPPORTED = -2
 HTN_ELAUNCH = -3
-SYNC_BYTES = 4096
+HEAD_SCRATCH_BYTES = 65536
 HEAD_DIM = 128
 
 _P = ctypes.c_void_p
@@ -46,9 +46,9 @@ SIGNATURES = {
                             _I64, _I64, _P],
     "htn_attention_scratch_bytes": [_I64, _I64, _I64, _I64],
     "htn_grouped_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
-                              _I64, _P, _P, _P],
+                              _I64, _P, _P],
     "htn_prologue_attention": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64, _I,
-                               _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P],
+                               _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64}
 
@@ -103,25 +103,3 @@ def require_gpu(*tensors):
     for t in tensors:
         if t is not None and not t.is_cuda:
             raise ValueError("hackthenorth_amd ops run on the GPU only; got a CPU tensor")
-
-
-_sync = {}
-
-
-def sync_buffer(device):
-    """Per-device zeroed completion-counter buffer (HTN_SYNC_BYTES).
-
-    The kernels that use it leave it zero, so it is allocated once, outside
-    any graph capture, and shared by every launch made in stream order.
-    """
-    index = torch.device(device).index
-    if index is None:
-        index = torch.cuda.current_device()
-    buf = _sync.get(index)
-    if buf is None:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("the sync buffer must be created before graph capture; "
-                               "run the op once eagerly first")
-        buf = torch.zeros(SYNC_BYTES, dtype=torch.uint8, device=torch.device("cuda", index))
-        _sync[index] = buf
-    return buf

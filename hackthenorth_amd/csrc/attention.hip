@@ -7,9 +7,10 @@
 //    query rows of its kv head once, streams its slice of K then V with
 //    16-byte loads (16 lanes per 256-byte cache row, four rows per wave
 //    instruction), keeps scores in LDS for an exact two-pass softmax, and
-//    writes an unnormalised partial plus (max, sum). The last block of each
-//    kv head (completion counter) merges the partials, so one launch covers
-//    split-KV and the log-sum-exp merge; the counter is reset by that block.
+//    writes an unnormalised partial plus (max, sum); a second launch merges
+//    the partials per output row (log-sum-exp weights). A block never waits
+//    for other blocks: an agent-scope release per block (L2 write-back on
+//    gfx950) costs far more than the extra launch.
 //  * slots after a query's absolute position are masked; slots after the
 //    largest position are never read.
 //  * the fused prologue variant computes q and the newest k/v from the packed
@@ -22,7 +23,6 @@ namespace htn {
 constexpr int D = HTN_HEAD_DIM;
 constexpr int kRowChunk = 8;        // query rows held in registers at once
 constexpr int kMaxRows = 32;        // G * Q
-constexpr int kSyncAttnOffset = 64; // attention counters start here in the sync buffer
 constexpr int kSlotUnroll = 4;      // 16-slot groups per wave: 64 slots per block pass
 constexpr int kMaxSplit = 16 * kSlotUnroll;
 constexpr int kMergeUnroll = 8;     // partials loaded back to back in the merge
@@ -107,7 +107,6 @@ struct AttnArgs {
   bf16_t* out;          // [B, Hq, Q, D]
   float* part;          // [B, Hq, Q, splits, D]
   float* ml;            // [B, Hq, Q, splits, 2]
-  unsigned* counters;   // [B * Hkv]
   int B, Hq, Hkv, G, Q, splits, split;
   float scale;
 };
@@ -123,7 +122,6 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   float* lrow = mrow + kMaxRows;                                  // [kMaxRows]
   bf16_t* knew = reinterpret_cast<bf16_t*>(lrow + kMaxRows);      // [D]
   bf16_t* vnew = knew + D;                                        // [D]
-  int* flag = reinterpret_cast<int*>(vnew + D);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane >> 4, e = lane & 15;
@@ -304,72 +302,65 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     }
   }
 
-  if (a.splits == 1) return;
+}
 
-  // ---- 6. the last block of this kv head merges the partials
-  __threadfence();
+// Merge of the split partials, one block per output row (b, h, t):
+//   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s,
+// over the splits that hold visible slots. Runs as its own launch after the
+// partial kernel, so the partials are visible without any in-kernel fence.
+__global__ __launch_bounds__(kBlock) void attention_merge(const float* __restrict__ part,
+                                                          const float* __restrict__ ml,
+                                                          const int64_t* __restrict__ pos, int Q,
+                                                          long cap, int split, int splits,
+                                                          bf16_t* __restrict__ out) {
+  __shared__ float red[4];
+  __shared__ float lsum[4];
+  __shared__ float2 accs[4][D / 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long orow = blockIdx.x;
+  int64_t maxpos = -1;
+  for (int t = 0; t < Q; ++t) maxpos = pos[t] > maxpos ? pos[t] : maxpos;
+  if (maxpos >= cap) maxpos = cap - 1;
+  const int nact = maxpos < 0 ? 0 : (static_cast<int>(maxpos / split) + 1 < splits
+                                         ? static_cast<int>(maxpos / split) + 1 : splits);
+  const float* mlr = ml + orow * splits * 2;
+  const float* pr = part + orow * splits * D;
+  float m = -INFINITY;
+  for (int i = tid; i < nact; i += kBlock) m = fmaxf(m, mlr[2 * i]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
   __syncthreads();
-  if (tid == 0) {
-    unsigned* ctr = a.counters + static_cast<long>(b) * a.Hkv + kvh;
-    flag[0] = atomicAdd(ctr, 1u) == static_cast<unsigned>(a.splits - 1);
-  }
-  __syncthreads();
-  if (!flag[0]) return;
-  __threadfence();
-  const int nact = static_cast<int>(maxpos / a.split) + 1 < a.splits
-                       ? static_cast<int>(maxpos / a.split) + 1 : a.splits;
-  // (a) per row: global max M and denominator L over the active splits
-  for (int r = wave; r < rows; r += 4) {
-    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-    const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
-    float m = -INFINITY;
-    for (int i = lane; i < nact; i += kWave) m = fmaxf(m, a.ml[(orow * a.splits + i) * 2]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int i = lane; i < nact; i += kWave) {
-      const float mi = a.ml[(orow * a.splits + i) * 2];
-      l += mi == -INFINITY ? 0.f : expf(mi - m) * a.ml[(orow * a.splits + i) * 2 + 1];
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      mrow[r] = m;
-      lrow[r] = l;
-    }
-  }
-  __syncthreads();
-  // (b) out = sum_s exp(m_s - M) acc_s / L, 4 dims per thread, loads unrolled
-  for (int i = tid; i < rows * (D / 4); i += kBlock) {
-    const int r = i / (D / 4), d4 = (i % (D / 4)) * 4;
-    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-    const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
-    const float m = mrow[r];
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < nact; s0 += kMergeUnroll) {
-      float4 pv[kMergeUnroll];
-      float mv[kMergeUnroll];
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float2 acc = make_float2(0.f, 0.f);
+  float l = 0.f;
+  for (int s0 = wave; s0 < nact; s0 += 4 * kMergeUnroll) {
+    float2 pv[kMergeUnroll];
+    float mv[kMergeUnroll], lv[kMergeUnroll];
 #pragma unroll
-      for (int u = 0; u < kMergeUnroll; ++u) {
-        const int sp = s0 + u < nact ? s0 + u : nact - 1;
-        pv[u] = *reinterpret_cast<const float4*>(a.part + (orow * a.splits + sp) * D + d4);
-        mv[u] = a.ml[(orow * a.splits + sp) * 2];
-      }
-#pragma unroll
-      for (int u = 0; u < kMergeUnroll; ++u) {
-        const float w = (s0 + u < nact && mv[u] != -INFINITY) ? expf(mv[u] - m) : 0.f;
-        v.x = fmaf(w, pv[u].x, v.x);
-        v.y = fmaf(w, pv[u].y, v.y);
-        v.z = fmaf(w, pv[u].z, v.z);
-        v.w = fmaf(w, pv[u].w, v.w);
-      }
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int sp = s0 + 4 * u;
+      const int sc = sp < nact ? sp : s0;
+      pv[u] = *reinterpret_cast<const float2*>(pr + static_cast<long>(sc) * D + 2 * lane);
+      mv[u] = sp < nact ? mlr[2 * sc] : -INFINITY;
+      lv[u] = mlr[2 * sc + 1];
     }
-    const float l = lrow[r];
-    bf16_t* o = a.out + orow * D + d4;
-    o[0] = static_cast<bf16_t>(f2bf(v.x / l));
-    o[1] = static_cast<bf16_t>(f2bf(v.y / l));
-    o[2] = static_cast<bf16_t>(f2bf(v.z / l));
-    o[3] = static_cast<bf16_t>(f2bf(v.w / l));
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const float w = mv[u] == -INFINITY ? 0.f : expf(mv[u] - m);
+      acc.x = fmaf(w, pv[u].x, acc.x);
+      acc.y = fmaf(w, pv[u].y, acc.y);
+      l = fmaf(w, lv[u], l);
+    }
   }
-  if (tid == 0) a.counters[static_cast<long>(b) * a.Hkv + kvh] = 0u;
+  accs[wave][lane] = acc;
+  if (lane == 0) lsum[wave] = l;
+  __syncthreads();
+  if (wave == 0) {
+    const float lt = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    const float2 a0 = accs[0][lane], a1 = accs[1][lane], a2 = accs[2][lane], a3 = accs[3][lane];
+    out[orow * D + 2 * lane] = static_cast<bf16_t>(f2bf(((a0.x + a1.x) + (a2.x + a3.x)) / lt));
+    out[orow * D + 2 * lane + 1] = static_cast<bf16_t>(f2bf(((a0.y + a1.y) + (a2.y + a3.y)) / lt));
+  }
 }
 
 // Split size: about two blocks per CU over (batch, kv head, split), slices of
@@ -399,16 +390,14 @@ using namespace htn;
 
 namespace {
 
-int run_attention(bool fused, AttnArgs& a, void* scratch, void* sync, hipStream_t st) {
+int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   const int rows = a.G * a.Q;
   if (rows <= 0 || rows > kMaxRows || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0) return HTN_EUNSUPPORTED;
-  if (static_cast<long>(a.B) * a.Hkv * 4 + kSyncAttnOffset > HTN_SYNC_BYTES) return HTN_EUNSUPPORTED;
   choose_split(a.B, a.Hkv, rows, a.cap, &a.split, &a.splits);
-  if (a.splits > 1 && (!scratch || !sync)) return HTN_EINVAL;
+  if (a.splits > 1 && !scratch) return HTN_EINVAL;
   const long nrow = static_cast<long>(a.B) * a.Hq * a.Q * a.splits;
   a.part = static_cast<float*>(scratch);
   a.ml = a.part ? a.part + nrow * D : nullptr;
-  a.counters = sync ? reinterpret_cast<unsigned*>(static_cast<char*>(sync) + kSyncAttnOffset) : nullptr;
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
   const dim3 grid(a.splits, a.Hkv, a.B);
   const size_t lds = attention_lds(rows, a.split);
@@ -416,6 +405,9 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, void* sync, hipStream_
     hipLaunchKernelGGL(attention_kernel<true>, grid, dim3(kBlock), lds, st, a);
   else
     hipLaunchKernelGGL(attention_kernel<false>, grid, dim3(kBlock), lds, st, a);
+  if (a.splits == 1 || launch_status() != HTN_OK) return launch_status();
+  hipLaunchKernelGGL(attention_merge, dim3(static_cast<long>(a.B) * a.Hq * a.Q), dim3(kBlock), 0, st,
+                     a.part, a.ml, a.pos, a.Q, a.cap, a.split, a.splits, a.out);
   return launch_status();
 }
 
@@ -467,7 +459,7 @@ extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, co
 extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                                      const void* keys, const void* values, int64_t cap,
                                      const int64_t* positions, void* out, int64_t B, int64_t Hq,
-                                     int64_t Hkv, int64_t Q, void* scratch, void* sync,
+                                     int64_t Hkv, int64_t Q, void* scratch,
                                      htn_stream_t stream) {
   if (!q || !keys || !values || !positions || !out) return HTN_EINVAL;
   if (Hkv <= 0 || Hq % Hkv != 0 || Q <= 0) return HTN_EINVAL;
@@ -478,7 +470,7 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
   a.cap = cap; a.pos = positions; a.out = static_cast<bf16_t*>(out);
   a.B = static_cast<int>(B); a.Hq = static_cast<int>(Hq); a.Hkv = static_cast<int>(Hkv);
   a.G = static_cast<int>(Hq / Hkv); a.Q = static_cast<int>(Q);
-  return run_attention(false, a, scratch, sync, static_cast<hipStream_t>(stream));
+  return run_attention(false, a, scratch, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off,
@@ -487,7 +479,7 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
                                       int64_t rope_st, int64_t rope_rows, int rope_by_position,
                                       void* keys, void* values, int64_t cap,
                                       const int64_t* positions, void* out, int64_t B,
-                                      int64_t Hkv, int64_t groups, void* scratch, void* sync,
+                                      int64_t Hkv, int64_t groups, void* scratch,
                                       htn_stream_t stream) {
   if (!qkv || !q_gain || !k_gain || !cos || !sin || !keys || !values || !positions || !out)
     return HTN_EINVAL;
@@ -502,5 +494,5 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
   a.cap = cap; a.pos = positions; a.out = static_cast<bf16_t*>(out);
   a.B = static_cast<int>(B); a.Hkv = static_cast<int>(Hkv); a.G = static_cast<int>(groups);
   a.Hq = static_cast<int>(Hkv * groups); a.Q = 1;
-  return run_attention(true, a, scratch, sync, static_cast<hipStream_t>(stream));
+  return run_attention(true, a, scratch, static_cast<hipStream_t>(stream));
 }

@@ -31,8 +31,7 @@ struct GemvArgs {
   bf16_t* y;
   int64_t* token_out;
   int64_t* position_inc;
-  uint64_t* slot;      // argmax key (sync buffer)
-  unsigned* counter;   // blocks finished (sync buffer)
+  uint64_t* partial;   // argmax: one key per block
   long n;              // output rows (gate rows for SwiGLU)
   int k;
   int kpad;            // k rounded up to 512
@@ -81,25 +80,36 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, bf16_t* xs, float* re
   __syncthreads();
 }
 
-// Finish the greedy head: block best -> global atomic max -> last block
-// publishes the token, bumps the position and clears the sync words.
-__device__ __forceinline__ void argmax_finish(const GemvArgs& a, uint64_t best, uint64_t* keys) {
+// Greedy head, stage 1: the block's best (logit, id) key goes to its own slot
+// of the partial array. A separate one-block kernel reduces the slots: an
+// in-kernel cross-block completion would need an agent-scope release per
+// block, which writes back L2 and costs far more than one extra launch.
+__device__ __forceinline__ void argmax_block(const GemvArgs& a, uint64_t best, uint64_t* keys) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) keys[wave] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
     uint64_t b = keys[0];
     for (int i = 1; i < kBlock / kWave; ++i) b = keys[i] > b ? keys[i] : b;
-    if (b != 0) atomicMax(reinterpret_cast<unsigned long long*>(a.slot), b);
-    __threadfence();
-    const unsigned done = atomicAdd(a.counter, 1u);
-    if (done == gridDim.x - 1) {
-      __threadfence();
-      const uint64_t k = atomicExch(reinterpret_cast<unsigned long long*>(a.slot), 0ull);
-      a.token_out[0] = static_cast<int64_t>(argmax_key_index(k));
-      if (a.position_inc) a.position_inc[0] += 1;
-      atomicExch(a.counter, 0u);
-    }
+    a.partial[blockIdx.x] = b;
+  }
+}
+
+// Greedy head, stage 2: one block reduces the per-block keys, publishes the
+// token and (decode step) advances the position.
+__global__ __launch_bounds__(kBlock) void argmax_finish(const uint64_t* __restrict__ partial, int n,
+                                                       int64_t* token_out, int64_t* position_inc) {
+  __shared__ uint64_t keys[4];
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < n; i += kBlock) best = partial[i] > best ? partial[i] : best;
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) keys[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = keys[0];
+    for (int i = 1; i < 4; ++i) b = keys[i] > b ? keys[i] : b;
+    token_out[0] = static_cast<int64_t>(argmax_key_index(b));
+    if (position_inc) position_inc[0] += 1;
   }
 }
 
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
       }
     }
   }
-  if (EPI == EPI_ARGMAX) argmax_finish(a, best, keys);
+  if (EPI == EPI_ARGMAX) argmax_block(a, best, keys);
 }
 
 // Generic fallback for row lengths that are not a multiple of 8 or unaligned
@@ -239,7 +249,7 @@ __global__ __launch_bounds__(kBlock) void gemv_scalar(GemvArgs a) {
       a.y[n] = static_cast<bf16_t>(f2bf(out));
     }
   }
-  if (EPI == EPI_ARGMAX) argmax_finish(a, best, keys);
+  if (EPI == EPI_ARGMAX) argmax_block(a, best, keys);
 }
 
 // Row-wise argmax over materialised bf16 logits: one block per row.
@@ -268,34 +278,43 @@ namespace {
 
 constexpr int kMaxK = 16384;
 
+constexpr long kMaxBlocks = HTN_HEAD_SCRATCH_BYTES / 8;
+
+long grid_for(long groups, long per_cu) {
+  long blocks = (groups + 3) / 4;
+  long cap = static_cast<long>(device_cus()) * per_cu;
+  if (cap > kMaxBlocks) cap = kMaxBlocks;
+  blocks = blocks < cap ? blocks : cap;
+  return blocks < 1 ? 1 : blocks;
+}
+
+int finish_argmax(const GemvArgs& a, long blocks, hipStream_t st) {
+  if (launch_status() != HTN_OK) return HTN_ELAUNCH;
+  hipLaunchKernelGGL(argmax_finish, dim3(1), dim3(kBlock), 0, st, a.partial,
+                     static_cast<int>(blocks), a.token_out, a.position_inc);
+  return launch_status();
+}
+
 template <int R, int S, int U, bool NORM, int EPI>
 int launch_vec(const GemvArgs& a, hipStream_t st) {
-  const long groups = (a.n + R - 1) / R;
-  long blocks = (groups + 3) / 4;
-  const long cap = static_cast<long>(device_cus()) * 8;
-  if (EPI == EPI_ARGMAX) {
-    // One atomic per block; keep the grid to a few blocks per CU.
-    const long c2 = static_cast<long>(device_cus()) * 4;
-    blocks = blocks < c2 ? blocks : c2;
-  }
-  blocks = blocks < cap ? blocks : cap;
-  if (blocks < 1) blocks = 1;
+  const long blocks = grid_for((a.n + R - 1) / R, 8);
   const size_t lds = static_cast<size_t>(a.kpad) * 2 + kLdsHead;
   hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
+  if (EPI == EPI_ARGMAX) return finish_argmax(a, blocks, st);
   return launch_status();
 }
 
 template <bool NORM, int EPI>
 int launch_scalar(const GemvArgs& a, hipStream_t st) {
-  long blocks = (a.n + 3) / 4;
-  const long cap = static_cast<long>(device_cus()) * 4;
-  blocks = blocks < cap ? blocks : cap;
+  const long blocks = grid_for(a.n, 4);
   const size_t lds = static_cast<size_t>(a.k) * 4 + kLdsHead;
   hipLaunchKernelGGL((gemv_scalar<NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
+  if (EPI == EPI_ARGMAX) return finish_argmax(a, blocks, st);
   return launch_status();
 }
 
-// Loads in flight per lane = U * R * S; aim for ~16 (64 VGPRs of weights).
+// One output row (gate/up pair for SwiGLU) per wave, so even 1024-row
+// projections spread over every CU; U 1 KB chunks per row in flight.
 template <bool NORM, int EPI>
 int dispatch(GemvArgs& a, hipStream_t st) {
   const bool vec = (a.k % 8 == 0) && aligned16(a.x) && aligned16(a.w) &&
@@ -304,9 +323,9 @@ int dispatch(GemvArgs& a, hipStream_t st) {
   a.kpad = (a.k + 511) / 512 * 512;
   const int chunks = a.kpad / 512;
   constexpr int S = EPI == EPI_SWIGLU ? 2 : 1;
-  if (chunks <= 2) return launch_vec<(S == 2 ? 4 : 8), S, 2, NORM, EPI>(a, st);
-  if (chunks <= 6) return launch_vec<(S == 2 ? 2 : 4), S, 4, NORM, EPI>(a, st);
-  return launch_vec<(S == 2 ? 1 : 2), S, 8, NORM, EPI>(a, st);
+  if (chunks <= 2) return launch_vec<1, S, 2, NORM, EPI>(a, st);
+  if (chunks <= 4) return launch_vec<1, S, 4, NORM, EPI>(a, st);
+  return launch_vec<1, S, 8, NORM, EPI>(a, st);
 }
 
 bool bad_sizes(int64_t n, int64_t k) { return n <= 0 || k <= 0 || k > kMaxK || n > (1L << 31); }
@@ -359,8 +378,8 @@ extern "C" int htn_gemv_residual(const void* x, const void* w, const void* resid
 
 extern "C" int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
                                   int64_t vocab, int64_t k, int64_t* token_out,
-                                  int64_t* position_inc, void* sync, htn_stream_t stream) {
-  if (!x || !w || !token_out || !sync || bad_sizes(vocab, k)) return HTN_EINVAL;
+                                  int64_t* position_inc, void* scratch, htn_stream_t stream) {
+  if (!x || !w || !token_out || !scratch || bad_sizes(vocab, k)) return HTN_EINVAL;
   GemvArgs a{};
   a.x = static_cast<const bf16_t*>(x);
   a.gain = static_cast<const bf16_t*>(gain);
@@ -370,8 +389,7 @@ extern "C" int htn_lm_head_argmax(const void* x, const void* gain, float eps, co
   a.eps = eps;
   a.token_out = token_out;
   a.position_inc = position_inc;
-  a.slot = static_cast<uint64_t*>(sync);
-  a.counter = reinterpret_cast<unsigned*>(static_cast<char*>(sync) + 8);
+  a.partial = static_cast<uint64_t*>(scratch);
   hipStream_t st = static_cast<hipStream_t>(stream);
   return gain ? dispatch<true, EPI_ARGMAX>(a, st) : dispatch<false, EPI_ARGMAX>(a, st);
 }

@@ -213,7 +213,7 @@ class DecodeState:
         stream = torch.cuda.Stream(device=model.device)
         stream.wait_stream(torch.cuda.current_stream(model.device))
         with torch.cuda.stream(stream):
-            # Library load, sync buffer and allocator warm-up happen off capture.
+            # Library load and allocator warm-up happen off capture.
             for _ in range(2):
                 self.position.fill_(prompt_length)
                 self.step(model)

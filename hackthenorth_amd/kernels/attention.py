@@ -41,7 +41,7 @@ def grouped_attention(q, k, v, positions):
     _lib.call("htn_grouped_attention", _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2),
               _lib.ptr(k), _lib.ptr(v), k.shape[2], _lib.ptr(positions.contiguous()),
               _lib.ptr(out), batch, heads, kv_heads, queries, _lib.ptr(scratch),
-              _lib.ptr(_lib.sync_buffer(q.device)), _lib.stream(q.device))
+              _lib.stream(q.device))
     return out
 
 
@@ -69,7 +69,7 @@ def _prologue(qkv, q_norm, k_norm, cos, sin, by_position, keys, values, position
               float(k_norm.variance_epsilon), _lib.ptr(cos), _lib.ptr(sin), _lib.HEAD_DIM,
               rope_rows, int(by_position), _lib.ptr(keys), _lib.ptr(values), keys.shape[2],
               _lib.ptr(positions), _lib.ptr(out), batch, kv_heads, groups, _lib.ptr(scratch),
-              _lib.ptr(_lib.sync_buffer(qkv.device)), _lib.stream(qkv.device))
+              _lib.stream(qkv.device))
     return out
 
 

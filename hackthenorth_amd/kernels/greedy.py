@@ -22,9 +22,9 @@ def greedy_head(x, gain, eps, w, out, advance=None):
     if out.dtype != torch.int64 or (advance is not None and advance.dtype != torch.int64):
         raise ValueError("token and position buffers must be int64")
     _lib.require_gpu(x, w, out)
-    sync = _lib.sync_buffer(x.device)
+    scratch = torch.empty(_lib.HEAD_SCRATCH_BYTES, dtype=torch.uint8, device=x.device)
     _lib.call("htn_lm_head_argmax", _lib.ptr(x), _lib.ptr(gain), float(eps), _lib.ptr(w),
-              w.shape[0], k, _lib.ptr(out), _lib.ptr(advance), _lib.ptr(sync),
+              w.shape[0], k, _lib.ptr(out), _lib.ptr(advance), _lib.ptr(scratch),
               _lib.stream(x.device))
     return out
 

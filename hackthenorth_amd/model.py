@@ -144,11 +144,22 @@ class Qwen3Model:
         return self.config.widths
 
     def weight_bytes(self):
+        """Bytes of all weight tensors resident in HBM."""
         total = self.embed_weight.numel() * 2
         if self.lm_head_weight is not self.embed_weight:
             total += self.lm_head_weight.numel() * 2
         for layer in self.layers:
             total += sum(t.numel() * 2 for t in layer.tensors().values())
+        return total
+
+    def decode_weight_bytes(self):
+        """Weight bytes one decode step must read: every projection and the LM
+        head once, plus the single embedding row and the norm gains."""
+        c = self.config
+        total = self.lm_head_weight.numel() * 2 + c.hidden_size * 2 * 2
+        for layer in self.layers:
+            total += sum(t.numel() * 2 for t in layer.tensors().values())
+            total += (2 * c.hidden_size + 2 * c.head_dim) * 2
         return total
 
     # ------------------------------------------------------------------ init

@@ -10,10 +10,11 @@
  * contiguous row-major. Positions and token ids are int64 device arrays that
  * the kernels read on the device (graph replays see updated values).
  *
- * "sync" buffers are caller-owned, zero-initialised device buffers of
- * HTN_SYNC_BYTES bytes holding completion counters; kernels leave them zero
- * again when they finish, so one buffer serves every call made in stream
- * order. Calls that run concurrently on one sync buffer race.
+ * "scratch" buffers are caller-owned device memory for per-block partial
+ * results, sized as each entry point states; no initial contents are
+ * required. Calls that run concurrently on one scratch buffer race.
+ * No kernel synchronises across its own blocks: every cross-block reduction
+ * is finished by a second, stream-ordered launch.
  *
  * Reference interfaces cited as file:line are in rickytang666/hackthenorth,
  * under dryft/engine/.
@@ -32,7 +33,7 @@ extern "C" {
 #define HTN_EUNSUPPORTED (-2) /* shape the kernels do not implement */
 #define HTN_ELAUNCH (-3)      /* the HIP launch failed */
 
-#define HTN_SYNC_BYTES 4096
+#define HTN_HEAD_SCRATCH_BYTES 65536
 #define HTN_HEAD_DIM 128
 
 typedef void* htn_stream_t;
@@ -103,13 +104,14 @@ int htn_gemv_residual(const void* x, const void* w, const void* residual, void* 
 /* Greedy head: token = argmax_n bf16(W[n] . xn) with the lowest id on ties,
  * where xn = x, or rms_norm(x, gain, eps) when gain is not NULL (the final
  * norm fused in). Writes token_out[0]; when position_inc is not NULL it also
- * adds 1 to position_inc[0] after every block has read it (the decode step's
- * position.add_(1)). `sync` is an HTN_SYNC_BYTES buffer.
+ * adds 1 to position_inc[0] (the decode step's position.add_(1)). Two
+ * launches: the GEMV leaves one key per block in `scratch`
+ * (HTN_HEAD_SCRATCH_BYTES), a one-block kernel reduces them.
  * Replaces greedy_token(x, w), kernels/greedy.py:45, and
  * lm_head(x).argmax(-1), decode.py:96-99. */
 int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
                        int64_t vocab, int64_t k, int64_t* token_out,
-                       int64_t* position_inc, void* sync, htn_stream_t stream);
+                       int64_t* position_inc, void* scratch, htn_stream_t stream);
 
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
@@ -145,13 +147,14 @@ int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t ca
  * absolute position: query t of head h sees slots <= positions[t] of kv head
  * h / (Hq / Hkv); later slots are never read. q[b, h, t, :] at
  * q + b*q_sb + h*q_sh + t*q_st; out is [B, Hq, Q, 128] contiguous.
- * Split-KV with the merge done by the last block of each kv head.
+ * Split-KV: one launch writes per-split partials to `scratch`
+ * (htn_attention_scratch_bytes), a second merges them (one launch when the
+ * context fits one split).
  * Replaces grouped_attention(q, k, v, positions), kernels/attention.py:213. */
 int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                           const void* keys, const void* values, int64_t cap,
                           const int64_t* positions, void* out, int64_t B, int64_t Hq,
-                          int64_t Hkv, int64_t Q, void* scratch, void* sync,
-                          htn_stream_t stream);
+                          int64_t Hkv, int64_t Q, void* scratch, htn_stream_t stream);
 
 /* Single-token decode attention with the QK-norm/RoPE/cache append fused in:
  * q, the newest k and v come from the packed projection row
@@ -166,7 +169,7 @@ int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64
                            int64_t rope_rows, int rope_by_position, void* keys, void* values,
                            int64_t cap,
                            const int64_t* positions, void* out, int64_t B, int64_t Hkv,
-                           int64_t groups, void* scratch, void* sync, htn_stream_t stream);
+                           int64_t groups, void* scratch, htn_stream_t stream);
 
 #ifdef __cplusplus
 }
