@@ -34,7 +34,6 @@ struct GemvArgs {
   uint64_t* partial;   // argmax: one key per block
   long n;              // output rows (gate rows for SwiGLU)
   int k;
-  int kpad;            // k rounded up to 512
   float eps;
 };
 
@@ -43,41 +42,6 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   float sig = 1.0f / (1.0f + expf(-g));
   float act = round_bf(g * sig);
   return act * u;
-}
-
-// Stage x (or its RMSNorm) into LDS as bf16, zero-padded to kpad.
-template <bool NORM>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, bf16_t* xs, float* red) {
-  const int tid = threadIdx.x;
-  const int kv = a.k >> 3, kvp = a.kpad >> 3;
-  float ss = 0.f;
-  for (int v = tid; v < kvp; v += kBlock) {
-    uint4 xv = make_uint4(0, 0, 0, 0);
-    if (v < kv) xv = *reinterpret_cast<const uint4*>(a.x + v * 8);
-    if (NORM) {
-      float f[8];
-      unpack8(xv, f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
-    }
-    *reinterpret_cast<uint4*>(xs + v * 8) = xv;
-  }
-  if (NORM) {
-    const float total = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(total / static_cast<float>(a.k) + a.eps);
-    for (int v = tid; v < kv; v += kBlock) {
-      float f[8], g[8];
-      unpack8(*reinterpret_cast<const uint4*>(xs + v * 8), f);
-      unpack8(*reinterpret_cast<const uint4*>(a.gain + v * 8), g);
-      uint4 o;
-      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
-      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
-      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
-      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
-      *reinterpret_cast<uint4*>(xs + v * 8) = o;
-    }
-  }
-  __syncthreads();
 }
 
 // Greedy head, stage 1: the block's best (logit, id) key goes to its own slot
@@ -113,10 +77,12 @@ __global__ __launch_bounds__(kBlock) void argmax_finish(const uint64_t* __restri
   }
 }
 
+// Weight batch: chunks c0 .. c0+U-1 of output rows n0 .. n0+R-1 (for SwiGLU
+// each is the pair gate row n, up row n + N). Lane l reads 16 bytes at vector
+// c*64 + l of each row; rows past the end re-read the last row (discarded).
 template <int R, int S, int U>
-__device__ __forceinline__ void issue_batch(const GemvArgs& a, long grp, int c0, int kv, int lane,
+__device__ __forceinline__ void issue_batch(const GemvArgs& a, long n0, int c0, int kv, int lane,
                                             uint4 (&wv)[U][R][S]) {
-  const long n0 = grp * R;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const long n = n0 + r < a.n ? n0 + r : a.n - 1;
@@ -132,13 +98,17 @@ __device__ __forceinline__ void issue_batch(const GemvArgs& a, long grp, int c0,
   }
 }
 
+// One wave per output row (row pair for SwiGLU), rows grid-strided over
+// persistent blocks. Lane l only ever multiplies activation vectors c*64 + l:
+// without the RMSNorm prologue they are loaded next to each weight batch (L1
+// hits after the CU's first wave) and the waves never synchronise; with it the
+// block normalises x once into LDS, amortised over all rows the block streams.
 template <int R, int S, int U, bool NORM, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
+  __shared__ uint64_t keys[kBlock / kWave];
+  __shared__ float red[kBlock / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
-  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
-  float* red = reinterpret_cast<float*>(smem + 64);
-  bf16_t* xs = reinterpret_cast<bf16_t*>(smem + kLdsHead);
-
+  bf16_t* xs = reinterpret_cast<bf16_t*>(smem);   // normalised x (NORM only)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kv = a.k >> 3;
   const int chunks = (kv + 63) >> 6;
@@ -146,12 +116,35 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   const long stride = static_cast<long>(gridDim.x) * 4;
   long grp = static_cast<long>(blockIdx.x) * 4 + wave;
 
-  // The first weight batch does not depend on x: issue it before the
-  // activation/RMSNorm prologue so the two latencies overlap.
+  // First weight batch before anything that waits on memory.
   uint4 wv[U][R][S];
   bool pending = grp < groups;
-  if (pending) issue_batch<R, S, U>(a, grp, 0, kv, lane, wv);
-  stage_x<NORM>(a, xs, red);
+  if (pending) issue_batch<R, S, U>(a, grp * R, 0, kv, lane, wv);
+
+  // RMSNorm prologue: the block normalises x once into LDS (bf16, rounded as
+  // the reference rounds) and its waves then stream many rows against it.
+  if constexpr (NORM) {
+    float ss = 0.f;
+    for (int v = threadIdx.x; v < kv; v += kBlock) {
+      float f[8];
+      unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+    const float inv = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(a.k) + a.eps);
+    for (int v = threadIdx.x; v < kv; v += kBlock) {
+      float f[8], g[8];
+      unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
+      unpack8(*reinterpret_cast<const uint4*>(a.gain + v * 8), g);
+      uint4 o;
+      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+      *reinterpret_cast<uint4*>(xs + v * 8) = o;
+    }
+    __syncthreads();
+  }
 
   uint64_t best = 0;
   for (; grp < groups; grp += stride) {
@@ -161,29 +154,33 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int s = 0; s < S; ++s) acc[r][s] = 0.f;
-
     for (int c0 = 0; c0 < chunks; c0 += U) {
-      if (!pending) issue_batch<R, S, U>(a, grp, c0, kv, lane, wv);
+      if (!pending) issue_batch<R, S, U>(a, n0, c0, kv, lane, wv);
       pending = false;
+      uint4 xv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (c0 + u < chunks) {
-          const int v = (c0 + u) * 64 + lane;
-          float xf[8];
-          unpack8(*reinterpret_cast<const uint4*>(xs + v * 8), xf);
+        const int v = (c0 + u) * 64 + lane;
+        if (NORM)
+          xv[u] = v < kv ? *reinterpret_cast<const uint4*>(xs + v * 8) : make_uint4(0, 0, 0, 0);
+        else
+          xv[u] = v < kv ? *reinterpret_cast<const uint4*>(a.x + v * 8) : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
-          for (int r = 0; r < R; ++r)
+      for (int u = 0; u < U; ++u) {
+        float xf[8];
+        unpack8(xv[u], xf);
 #pragma unroll
-            for (int s = 0; s < S; ++s) acc[r][s] += dot8(wv[u][r][s], xf);
-        }
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int s = 0; s < S; ++s) acc[r][s] += dot8(wv[u][r][s], xf);
       }
     }
-
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const long n = n0 + r;
-      float t0 = wave_sum(acc[r][0]);
-      float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
+      const float t0 = wave_sum(acc[r][0]);
+      const float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
       if (n < a.n) {
         if (EPI == EPI_ARGMAX) {
           const uint64_t key = argmax_key(f2bf(t0), static_cast<uint32_t>(n));
@@ -295,10 +292,19 @@ int finish_argmax(const GemvArgs& a, long blocks, hipStream_t st) {
   return launch_status();
 }
 
+// Waves resident per CU at full occupancy of 4 blocks (16 waves).
+constexpr long kWavesPerCu = 16;
+
 template <int R, int S, int U, bool NORM, int EPI>
 int launch_vec(const GemvArgs& a, hipStream_t st) {
-  const long blocks = grid_for((a.n + R - 1) / R, 8);
-  const size_t lds = static_cast<size_t>(a.kpad) * 2 + kLdsHead;
+  const long groups = (a.n + R - 1) / R;
+  // RMSNorm kernels pay their prologue once per block: when every wave would
+  // stream three or more row groups anyway, two longer-lived blocks per CU
+  // beat four. Kernels without a prologue fill the CU.
+  long per_cu = 8;
+  if (NORM) per_cu = groups >= 3 * kWavesPerCu * device_cus() ? 2 : 4;
+  const long blocks = grid_for(groups, per_cu);
+  const size_t lds = NORM ? static_cast<size_t>(a.k) * 2 : 0;
   hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
   if (EPI == EPI_ARGMAX) return finish_argmax(a, blocks, st);
   return launch_status();
@@ -313,17 +319,22 @@ int launch_scalar(const GemvArgs& a, hipStream_t st) {
   return launch_status();
 }
 
-// One output row (gate/up pair for SwiGLU) per wave, so even 1024-row
-// projections spread over every CU; U 1 KB chunks per row in flight.
+// One output row (gate/up pair for SwiGLU) per wave by default, so even
+// 1024-row projections spread over every CU, with U 1 KB chunks per row in
+// flight. Short rows (K <= 1024) over many rows take four rows per wave so a
+// wave still keeps 8 KB of loads in flight.
 template <bool NORM, int EPI>
 int dispatch(GemvArgs& a, hipStream_t st) {
   const bool vec = (a.k % 8 == 0) && aligned16(a.x) && aligned16(a.w) &&
                    (!NORM || aligned16(a.gain));
   if (!vec) return launch_scalar<NORM, EPI>(a, st);
-  a.kpad = (a.k + 511) / 512 * 512;
-  const int chunks = a.kpad / 512;
+  const int chunks = (a.k + 511) / 512;
   constexpr int S = EPI == EPI_SWIGLU ? 2 : 1;
-  if (chunks <= 2) return launch_vec<1, S, 2, NORM, EPI>(a, st);
+  const bool many_rows = a.n >= 4 * kWavesPerCu * device_cus();
+  if (chunks <= 2) {
+    if (S == 1 && many_rows) return launch_vec<4, S, 2, NORM, EPI>(a, st);
+    return launch_vec<1, S, 2, NORM, EPI>(a, st);
+  }
   if (chunks <= 4) return launch_vec<1, S, 4, NORM, EPI>(a, st);
   return launch_vec<1, S, 8, NORM, EPI>(a, st);
 }
