@@ -21,10 +21,9 @@
 namespace htn {
 
 constexpr int D = HTN_HEAD_DIM;
-constexpr int kRowChunk = 8;        // query rows held in registers at once
 constexpr int kMaxRows = 32;        // G * Q
-constexpr int kSlotUnroll = 4;      // 16-slot groups per wave: 64 slots per block pass
-constexpr int kMaxSplit = 16 * kSlotUnroll;
+constexpr int kSplit = 64;          // cache slots per block
+constexpr int kMaxQ = 8;            // queries per launch (verify rows)
 constexpr int kMergeUnroll = 8;     // partials loaded back to back in the merge
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
@@ -111,75 +110,142 @@ struct AttnArgs {
   float scale;
 };
 
-template <bool FUSED>
-__global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int rows = a.G * a.Q;
-  float* qs = reinterpret_cast<float*>(smem);                     // [rows][D]
-  float* sc = qs + rows * D;                                      // [rows][kMaxSplit]
-  float* accr = sc + rows * kMaxSplit;                            // [4][kRowChunk][D]
-  float* mrow = accr + 4 * kRowChunk * D;                         // [kMaxRows]
-  float* lrow = mrow + kMaxRows;                                  // [kMaxRows]
-  bf16_t* knew = reinterpret_cast<bf16_t*>(lrow + kMaxRows);      // [D]
-  bf16_t* vnew = knew + D;                                        // [D]
+// Per-head RMSNorm + RoPE for a 32-lane half wave: lane l of the half owns
+// elements l, l+32, l+64, l+96, i.e. the rotate_half pairs (l, l+64) and
+// (l+32, l+96). Loads are issued by norm_rope_load, math by norm_rope_math, so
+// a caller can put the loads ahead of its other memory traffic.
+struct HeadLoads {
+  float x[4], g[4], c[4], s[4];
+};
+
+__device__ __forceinline__ void norm_rope_load(const bf16_t* x, const bf16_t* g, const bf16_t* cs,
+                                               const bf16_t* sn, int hl, HeadLoads& h) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = hl + 32 * i;
+    h.x[i] = bf2f(x[e]);
+    h.g[i] = bf2f(g[e]);
+    h.c[i] = bf2f(cs[e]);
+    h.s[i] = bf2f(sn[e]);
+  }
+}
+
+// Sum over the 32 lanes of each half wave (lanes 0-31 and 32-63 separately).
+__device__ __forceinline__ float half_sum(float v, int lane) {
+  v = row16_sum(v);
+  const float lo = readlane(v, 0) + readlane(v, 16);
+  const float hi = readlane(v, 32) + readlane(v, 48);
+  return lane < 32 ? lo : hi;
+}
+
+__device__ __forceinline__ void norm_rope_math(const HeadLoads& h, float eps, int lane,
+                                               float (&o)[4]) {
+  const float ss =
+      half_sum((h.x[0] * h.x[0] + h.x[1] * h.x[1]) + (h.x[2] * h.x[2] + h.x[3] * h.x[3]), lane);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+  float n[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) n[i] = round_bf(h.g[i] * round_bf(h.x[i] * inv));
+  // element e < 64 pairs with e + 64 (rot = -n[e+64]); e >= 64 with e - 64 (rot = n[e-64])
+  o[0] = round_bf(round_bf(n[0] * h.c[0]) + round_bf(-n[2] * h.s[0]));
+  o[1] = round_bf(round_bf(n[1] * h.c[1]) + round_bf(-n[3] * h.s[1]));
+  o[2] = round_bf(round_bf(n[2] * h.c[2]) + round_bf(n[0] * h.s[2]));
+  o[3] = round_bf(round_bf(n[3] * h.c[3]) + round_bf(n[1] * h.s[3]));
+}
+
+// Split-KV partial attention for one (split of 64 slots, kv head, batch).
+// ROWS query rows (G heads x Q queries) are processed per chunk; K is read
+// with 16 lanes per 256-byte row (dot products finish with DPP row sums), V
+// with one wave per 16 slots and 4 bytes per lane (P.V needs no cross-lane
+// reduction). Splits past the last position write neutral partials
+// (max -inf, sum 0) so the merge never needs the positions.
+template <int ROWS, bool FUSED>
+__global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
+  __shared__ float qs[kMaxRows * D];
+  __shared__ float sc[ROWS * kSplit];
+  __shared__ float accr[4 * ROWS * D];
+  __shared__ float mrow[ROWS], lrow[ROWS];
+  __shared__ __align__(16) bf16_t knew[D];
+  __shared__ __align__(16) bf16_t vnew[D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane >> 4, e = lane & 15;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int rows = a.G * a.Q;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
 
+  int64_t qp[kMaxQ];
   int64_t maxpos = -1;
-  for (int t = 0; t < a.Q; ++t) maxpos = a.pos[t] > maxpos ? a.pos[t] : maxpos;
-  if (maxpos >= a.cap) maxpos = a.cap - 1;
-  const long start = static_cast<long>(s) * a.split;
-  long end = start + a.split;
-  if (end > maxpos + 1) end = maxpos + 1;
-  const bool active = start <= maxpos;
-  const int64_t newest = FUSED ? a.pos[0] : -1;
-
-  // ---- 1. issue this block's K and V loads first: they depend only on the
-  // positions, so their HBM latency overlaps the query prologue. Lane (sub, e)
-  // of wave w owns slot start + u*16 + w*4 + sub, dims e*8 .. e*8+7.
-  uint4 kreg[kSlotUnroll], vreg[kSlotUnroll];
 #pragma unroll
-  for (int u = 0; u < kSlotUnroll; ++u) {
-    const long j = start + u * 16 + wave * 4 + sub;
-    kreg[u] = make_uint4(0, 0, 0, 0);
-    vreg[u] = make_uint4(0, 0, 0, 0);
-    if (active && j < end && !(FUSED && j == newest)) {
+  for (int t = 0; t < kMaxQ; ++t) {
+    qp[t] = t < a.Q ? a.pos[t] : -1;
+    maxpos = qp[t] > maxpos ? qp[t] : maxpos;
+  }
+  if (maxpos >= a.cap) maxpos = a.cap - 1;
+  const long start = static_cast<long>(s) * kSplit;
+  const long end = start + kSplit < maxpos + 1 ? start + kSplit : maxpos + 1;
+  const bool active = start <= maxpos;
+  const int64_t newest = FUSED ? qp[0] : -1;
+  const bool has_newest = FUSED && active && newest >= start && newest < end;
+
+  // ---- 1. prologue loads first (they gate the query rows), then K and V.
+  // Every load is unconditional with its index clamped into valid memory:
+  // loads under per-lane conditions serialise (one wait per load).
+  const int hl = lane & 31, half = lane >> 5;
+  const int head_slot = wave * 2 + half;  // 8 head slots per block: G query heads, then k
+  HeadLoads hq;
+  const bf16_t* qrow = nullptr;
+  bool do_head = false, is_k = false;
+  if (FUSED) {
+    const long rr = a.rope_by_pos ? newest : 0;
+    const long ri = (rr >= 0 && rr < a.rope_rows) ? rr : 0;
+    const bf16_t* cs = a.cos + ri * a.rope_st;
+    const bf16_t* sn = a.sin + ri * a.rope_st;
+    qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
+    is_k = head_slot == a.G;
+    do_head = head_slot < a.G || (is_k && has_newest);
+    const int hs = head_slot < a.G ? head_slot : 0;
+    const bf16_t* src = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
+                             : qrow + (static_cast<long>(kvh) * a.G + hs) * D;
+    norm_rope_load(src, is_k ? a.kg : a.qg, cs, sn, hl, hq);
+  }
+  uint4 kreg[4];
+  uint32_t vreg[16];
+  if (active) {  // block-uniform
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      long j = start + u * 16 + wave * 4 + sub;
+      j = j < end ? j : end - 1;
       kreg[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
-      vreg[u] = *reinterpret_cast<const uint4*>(a.values + kv_base + j * D + e * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      long j = start + wave * 16 + i;
+      j = j < end ? j : end - 1;
+      vreg[i] = *reinterpret_cast<const uint32_t*>(a.values + kv_base + j * D + 2 * lane);
     }
   }
 
   // ---- 2. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
-    const long rr = a.rope_by_pos ? newest : 0;
-    const bool rope_ok = rr >= 0 && rr < a.rope_rows;
-    const bf16_t* cs = a.cos + (rope_ok ? rr : 0) * a.rope_st;
-    const bf16_t* sn = a.sin + (rope_ok ? rr : 0) * a.rope_st;
-    const bf16_t* row = a.qkv + static_cast<long>(b) * a.qkv_sb;
-    for (int g = wave; g < a.G; g += 4) {
-      float o0, o1;
-      norm_rope_wave(row + (static_cast<long>(kvh) * a.G + g) * D, a.qg, a.q_eps, cs, sn, lane, o0, o1);
-      qs[g * D + lane] = o0;
-      qs[g * D + lane + 64] = o1;
-    }
-    if (wave == (a.G & 3) && active && newest >= start && newest < end) {
-      float o0, o1;
-      norm_rope_wave(row + a.k_off + static_cast<long>(kvh) * D, a.kg, a.k_eps, cs, sn, lane, o0, o1);
-      const bf16_t* vsrc = row + a.v_off + static_cast<long>(kvh) * D;
-      const bf16_t k0 = static_cast<bf16_t>(f2bf(o0)), k1 = static_cast<bf16_t>(f2bf(o1));
-      const bf16_t v0 = vsrc[lane], v1 = vsrc[lane + 64];
-      knew[lane] = k0;
-      knew[lane + 64] = k1;
-      vnew[lane] = v0;
-      vnew[lane + 64] = v1;
+    float o[4];
+    norm_rope_math(hq, is_k ? a.k_eps : a.q_eps, lane, o);
+    if (do_head && !is_k) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qs[head_slot * D + hl + 32 * i] = o[i];
+    } else if (do_head) {
       const long slot = kv_base + newest * D;
-      a.keys[slot + lane] = k0;
-      a.keys[slot + lane + 64] = k1;
-      a.values[slot + lane] = v0;
-      a.values[slot + lane + 64] = v1;
+      const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int el = hl + 32 * i;
+        const bf16_t kb = static_cast<bf16_t>(f2bf(o[i]));
+        const bf16_t vb = vsrc[el];
+        knew[el] = kb;
+        vnew[el] = vb;
+        a.keys[slot + el] = kb;
+        a.values[slot + el] = vb;
+      }
     }
   } else {
     for (int i = tid; i < rows * D; i += kBlock) {
@@ -190,198 +256,185 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-
-  const int len = active ? static_cast<int>(end - start) : 0;
-  if (active) {
-    if (FUSED && newest >= start && newest < end) {
+  if (has_newest) {  // block-uniform: the newest slot's k/v come from LDS, not memory
+    const uint4 kn = *reinterpret_cast<const uint4*>(knew + e * 8);
+    const uint32_t vn = *reinterpret_cast<const uint32_t*>(vnew + 2 * lane);
+    // Match on the clamped index: lanes past the end loaded slot end - 1,
+    // which is the newest slot itself.
 #pragma unroll
-      for (int u = 0; u < kSlotUnroll; ++u) {
-        if (start + u * 16 + wave * 4 + sub == newest) {
-          kreg[u] = *reinterpret_cast<const uint4*>(knew + e * 8);
-          vreg[u] = *reinterpret_cast<const uint4*>(vnew + e * 8);
-        }
-      }
+    for (int u = 0; u < 4; ++u) {
+      const long j = start + u * 16 + wave * 4 + sub;
+      const bool hit = (j < end ? j : end - 1) == newest;
+      kreg[u].x = hit ? kn.x : kreg[u].x;
+      kreg[u].y = hit ? kn.y : kreg[u].y;
+      kreg[u].z = hit ? kn.z : kreg[u].z;
+      kreg[u].w = hit ? kn.w : kreg[u].w;
     }
-    // ---- 3. scores q.k * D^-1/2 into LDS (16 lanes per slot, DPP row sums)
-    for (int r0 = 0; r0 < rows; r0 += kRowChunk) {
-      const int nr = rows - r0 < kRowChunk ? rows - r0 : kRowChunk;
-      float qr[kRowChunk][8];
 #pragma unroll
-      for (int r = 0; r < kRowChunk; ++r)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qr[r][i] = r < nr ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
-#pragma unroll
-      for (int u = 0; u < kSlotUnroll; ++u) {
-        const long j = start + u * 16 + wave * 4 + sub;
-#pragma unroll
-        for (int r = 0; r < kRowChunk; ++r) {
-          if (r < nr) {
-            const float dsum = row16_sum(dot8(kreg[u], qr[r]));
-            if (e == 0 && j < end) {
-              const int rr = r0 + r;
-              const int64_t qpos = a.pos[rr % a.Q];
-              sc[rr * kMaxSplit + (j - start)] = j <= qpos ? dsum * a.scale : -INFINITY;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-
-    // ---- 4. exact softmax numerators per row (the split's own max)
-    for (int r = wave; r < rows; r += 4) {
-      const float v = lane < len ? sc[r * kMaxSplit + lane] : -INFINITY;
-      const float m = wave_max(v);
-      const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
-      if (lane < len) sc[r * kMaxSplit + lane] = p;
-      const float l = wave_sum(p);
-      if (lane == 0) {
-        mrow[r] = m;
-        lrow[r] = l;
-      }
-    }
-    __syncthreads();
-
-    // ---- 5. P.V from the V rows already in registers
-    for (int r0 = 0; r0 < rows; r0 += kRowChunk) {
-      const int nr = rows - r0 < kRowChunk ? rows - r0 : kRowChunk;
-      float acc[kRowChunk][8];
-#pragma unroll
-      for (int r = 0; r < kRowChunk; ++r)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[r][i] = 0.f;
-#pragma unroll
-      for (int u = 0; u < kSlotUnroll; ++u) {
-        const long j = start + u * 16 + wave * 4 + sub;
-        if (j < end) {
-          float vf[8];
-          unpack8(vreg[u], vf);
-#pragma unroll
-          for (int r = 0; r < kRowChunk; ++r) {
-            if (r < nr) {
-              const float p = sc[(r0 + r) * kMaxSplit + (j - start)];
-#pragma unroll
-              for (int i = 0; i < 8; ++i) acc[r][i] = fmaf(p, vf[i], acc[r][i]);
-            }
-          }
-        }
-      }
-      // fold the four slot rows of the wave, then the four waves through LDS
-#pragma unroll
-      for (int r = 0; r < kRowChunk; ++r)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          acc[r][i] += __shfl_xor(acc[r][i], 16, kWave);
-          acc[r][i] += __shfl_xor(acc[r][i], 32, kWave);
-        }
-      if (sub == 0) {
-#pragma unroll
-        for (int r = 0; r < kRowChunk; ++r)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) accr[(wave * kRowChunk + r) * D + e * 8 + i] = acc[r][i];
-      }
-      __syncthreads();
-      for (int i = tid; i < nr * D; i += kBlock) {
-        const int r = i / D, d = i % D;
-        const float v = (accr[(0 * kRowChunk + r) * D + d] + accr[(1 * kRowChunk + r) * D + d]) +
-                        (accr[(2 * kRowChunk + r) * D + d] + accr[(3 * kRowChunk + r) * D + d]);
-        const int rr = r0 + r;
-        const int h = kvh * a.G + rr / a.Q, t = rr % a.Q;
-        const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
-        if (a.splits == 1) {
-          a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrow[rr]));
-        } else {
-          a.part[(orow * a.splits + s) * D + d] = v;
-          if (d == 0) {
-            a.ml[(orow * a.splits + s) * 2] = mrow[rr];
-            a.ml[(orow * a.splits + s) * 2 + 1] = lrow[rr];
-          }
-        }
-      }
-      __syncthreads();
+    for (int i = 0; i < 16; ++i) {
+      const long j = start + wave * 16 + i;
+      vreg[i] = (j < end ? j : end - 1) == newest ? vn : vreg[i];
     }
   }
 
+  const int len = active ? static_cast<int>(end - start) : 0;
+  for (int r0 = 0; r0 < rows; r0 += ROWS) {
+    float acc[ROWS][2];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.f;
+    if (active) {
+      // ---- 3. scores q.k * D^-1/2 (rows past `rows` compute on zeros, never stored)
+      float qr[ROWS][8];
+      int64_t rp[ROWS];
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) {
+        const bool ok = r0 + r < rows;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qr[r][i] = ok ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
+        rp[r] = -1;
+#pragma unroll
+        for (int t = 0; t < kMaxQ; ++t)
+          if (ok && t == (r0 + r) % a.Q) rp[r] = qp[t];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const long j = start + u * 16 + wave * 4 + sub;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+          const float dsum = row16_sum(dot8(kreg[u], qr[r]));
+          if (e == 0 && j < end) sc[r * kSplit + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
+        }
+      }
+      __syncthreads();
+      // ---- 4. exact softmax numerators per row over this split
+#pragma unroll
+      for (int r = wave; r < ROWS; r += 4) {
+        const float v = lane < len ? sc[r * kSplit + lane] : -INFINITY;
+        const float m = wave_max(v);
+        const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
+        sc[r * kSplit + lane] = p;
+        const float l = wave_sum(p);
+        if (lane == 0) {
+          mrow[r] = m;
+          lrow[r] = l;
+        }
+      }
+      __syncthreads();
+      // ---- 5. P.V: wave w owns slots w*16 .. w*16+15 of the split, each lane 2 dims;
+      // slots past the end carry p = 0 and a clamped (finite) V row.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int js = wave * 16 + i;
+        const float v0 = bf_lo(vreg[i]), v1 = bf_hi(vreg[i]);
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+          const float p = sc[r * kSplit + js];
+          acc[r][0] = fmaf(p, v0, acc[r][0]);
+          acc[r][1] = fmaf(p, v1, acc[r][1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = wave; r < ROWS; r += 4) {
+        if (lane == 0) {
+          mrow[r] = -INFINITY;
+          lrow[r] = 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      accr[(wave * ROWS + r) * D + 2 * lane] = acc[r][0];
+      accr[(wave * ROWS + r) * D + 2 * lane + 1] = acc[r][1];
+    }
+    __syncthreads();
+    for (int i = tid; i < ROWS * D; i += kBlock) {
+      const int r = i / D, d = i % D;
+      const int rr = r0 + r;
+      if (rr < rows) {
+        const float v = (accr[(0 * ROWS + r) * D + d] + accr[(1 * ROWS + r) * D + d]) +
+                        (accr[(2 * ROWS + r) * D + d] + accr[(3 * ROWS + r) * D + d]);
+        const int h = kvh * a.G + rr / a.Q, t = rr % a.Q;
+        const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
+        if (a.splits == 1) {
+          a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrow[r]));
+        } else {
+          a.part[(orow * a.splits + s) * D + d] = v;
+          if (d == 0) {
+            a.ml[(orow * a.splits + s) * 2] = mrow[r];
+            a.ml[(orow * a.splits + s) * 2 + 1] = lrow[r];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // Merge of the split partials, one block per output row (b, h, t):
-//   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s,
-// over the splits that hold visible slots. Runs as its own launch after the
-// partial kernel, so the partials are visible without any in-kernel fence.
+//   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
+// Each wave folds every fourth split with an online max (one pass over the
+// partials, loads unrolled), then the four wave states combine in LDS. It runs
+// as its own launch, so the partials are visible without any in-kernel fence.
 __global__ __launch_bounds__(kBlock) void attention_merge(const float* __restrict__ part,
-                                                          const float* __restrict__ ml,
-                                                          const int64_t* __restrict__ pos, int Q,
-                                                          long cap, int split, int splits,
+                                                          const float* __restrict__ ml, int splits,
                                                           bf16_t* __restrict__ out) {
-  __shared__ float red[4];
-  __shared__ float lsum[4];
-  __shared__ float2 accs[4][D / 2];
+  __shared__ float wm[4], wl[4];
+  __shared__ float2 wacc[4][D / 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long orow = blockIdx.x;
-  int64_t maxpos = -1;
-  for (int t = 0; t < Q; ++t) maxpos = pos[t] > maxpos ? pos[t] : maxpos;
-  if (maxpos >= cap) maxpos = cap - 1;
-  const int nact = maxpos < 0 ? 0 : (static_cast<int>(maxpos / split) + 1 < splits
-                                         ? static_cast<int>(maxpos / split) + 1 : splits);
   const float* mlr = ml + orow * splits * 2;
   const float* pr = part + orow * splits * D;
-  float m = -INFINITY;
-  for (int i = tid; i < nact; i += kBlock) m = fmaxf(m, mlr[2 * i]);
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float m = -INFINITY, l = 0.f;
   float2 acc = make_float2(0.f, 0.f);
-  float l = 0.f;
-  for (int s0 = wave; s0 < nact; s0 += 4 * kMergeUnroll) {
+  for (int s0 = wave; s0 < splits; s0 += 4 * kMergeUnroll) {
     float2 pv[kMergeUnroll];
     float mv[kMergeUnroll], lv[kMergeUnroll];
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u) {
       const int sp = s0 + 4 * u;
-      const int sc = sp < nact ? sp : s0;
+      const int sc = sp < splits ? sp : s0;
       pv[u] = *reinterpret_cast<const float2*>(pr + static_cast<long>(sc) * D + 2 * lane);
-      mv[u] = sp < nact ? mlr[2 * sc] : -INFINITY;
+      mv[u] = sp < splits ? mlr[2 * sc] : -INFINITY;
       lv[u] = mlr[2 * sc + 1];
     }
+    float mb = m;
 #pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) {
-      const float w = mv[u] == -INFINITY ? 0.f : expf(mv[u] - m);
-      acc.x = fmaf(w, pv[u].x, acc.x);
-      acc.y = fmaf(w, pv[u].y, acc.y);
-      l = fmaf(w, lv[u], l);
+    for (int u = 0; u < kMergeUnroll; ++u) mb = fmaxf(mb, mv[u]);
+    if (mb != -INFINITY) {
+      const float scale = m == -INFINITY ? 0.f : expf(m - mb);
+      acc.x *= scale;
+      acc.y *= scale;
+      l *= scale;
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        const float w = mv[u] == -INFINITY ? 0.f : expf(mv[u] - mb);
+        acc.x = fmaf(w, pv[u].x, acc.x);
+        acc.y = fmaf(w, pv[u].y, acc.y);
+        l = fmaf(w, lv[u], l);
+      }
+      m = mb;
     }
   }
-  accs[wave][lane] = acc;
-  if (lane == 0) lsum[wave] = l;
+  wacc[wave][lane] = acc;
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
   __syncthreads();
   if (wave == 0) {
-    const float lt = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
-    const float2 a0 = accs[0][lane], a1 = accs[1][lane], a2 = accs[2][lane], a3 = accs[3][lane];
-    out[orow * D + 2 * lane] = static_cast<bf16_t>(f2bf(((a0.x + a1.x) + (a2.x + a3.x)) / lt));
-    out[orow * D + 2 * lane + 1] = static_cast<bf16_t>(f2bf(((a0.y + a1.y) + (a2.y + a3.y)) / lt));
+    const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float sx = 0.f, sy = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = wm[w] == -INFINITY ? 0.f : expf(wm[w] - M);
+      sx = fmaf(f, wacc[w][lane].x, sx);
+      sy = fmaf(f, wacc[w][lane].y, sy);
+      lt = fmaf(f, wl[w], lt);
+    }
+    out[orow * D + 2 * lane] = static_cast<bf16_t>(f2bf(sx / lt));
+    out[orow * D + 2 * lane + 1] = static_cast<bf16_t>(f2bf(sy / lt));
   }
-}
-
-// Split size: about two blocks per CU over (batch, kv head, split), slices of
-// 32..64 cache slots (a 64-slot slice is one register-resident pass: four
-// 16-slot groups per wave).
-void choose_split(long B, long Hkv, long rows, long cap, int* split, int* splits) {
-  const long target = 2L * device_cus();
-  long per_head = target / (B * Hkv);
-  if (per_head < 1) per_head = 1;
-  const long want = (cap + per_head - 1) / per_head;
-  long sz = 32;
-  while (sz < want && sz < kMaxSplit) sz <<= 1;
-  (void)rows;
-  *split = static_cast<int>(sz);
-  *splits = static_cast<int>((cap + sz - 1) / sz);
-}
-
-size_t attention_lds(int rows, int split) {
-  (void)split;
-  return static_cast<size_t>(rows) * D * 4 + static_cast<size_t>(rows) * kMaxSplit * 4 +
-         4 * kRowChunk * D * 4 + 2 * kMaxRows * 4 + 2 * D * 2 + 16;
 }
 
 }  // namespace htn
@@ -390,24 +443,34 @@ using namespace htn;
 
 namespace {
 
+template <int ROWS>
+void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
+  const dim3 grid(a.splits, a.Hkv, a.B);
+  if (fused)
+    hipLaunchKernelGGL((attention_partial<ROWS, true>), grid, dim3(kBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((attention_partial<ROWS, false>), grid, dim3(kBlock), 0, st, a);
+}
+
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   const int rows = a.G * a.Q;
-  if (rows <= 0 || rows > kMaxRows || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0) return HTN_EUNSUPPORTED;
-  choose_split(a.B, a.Hkv, rows, a.cap, &a.split, &a.splits);
+  if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
+    return HTN_EUNSUPPORTED;
+  if (fused && a.G + 1 > 8) return HTN_EUNSUPPORTED;  // 8 head slots in the fused prologue
+  a.split = kSplit;
+  a.splits = static_cast<int>((a.cap + kSplit - 1) / kSplit);
   if (a.splits > 1 && !scratch) return HTN_EINVAL;
   const long nrow = static_cast<long>(a.B) * a.Hq * a.Q * a.splits;
   a.part = static_cast<float*>(scratch);
   a.ml = a.part ? a.part + nrow * D : nullptr;
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
-  const dim3 grid(a.splits, a.Hkv, a.B);
-  const size_t lds = attention_lds(rows, a.split);
-  if (fused)
-    hipLaunchKernelGGL(attention_kernel<true>, grid, dim3(kBlock), lds, st, a);
-  else
-    hipLaunchKernelGGL(attention_kernel<false>, grid, dim3(kBlock), lds, st, a);
+  if (rows <= 1) launch_partial<1>(fused, a, st);
+  else if (rows <= 2) launch_partial<2>(fused, a, st);
+  else if (rows <= 4) launch_partial<4>(fused, a, st);
+  else launch_partial<8>(fused, a, st);
   if (a.splits == 1 || launch_status() != HTN_OK) return launch_status();
-  hipLaunchKernelGGL(attention_merge, dim3(static_cast<long>(a.B) * a.Hq * a.Q), dim3(kBlock), 0, st,
-                     a.part, a.ml, a.pos, a.Q, a.cap, a.split, a.splits, a.out);
+  hipLaunchKernelGGL(attention_merge, dim3(static_cast<long>(a.B) * a.Hq * a.Q), dim3(kBlock), 0,
+                     st, a.part, a.ml, a.splits, a.out);
   return launch_status();
 }
 
@@ -415,13 +478,8 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
 
 extern "C" int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap) {
   if (B <= 0 || Hq <= 0 || Q <= 0 || cap <= 0) return 0;
-  // Worst case over kv-head counts dividing Hq: the split grows with Hkv * B.
-  int split = 0, splits = 0;
-  choose_split(B, 1, Hq * Q, cap, &split, &splits);
-  int split_min = 32;
-  const long most = (cap + split_min - 1) / split_min;
-  const long n = static_cast<long>(B) * Hq * Q * (most > splits ? most : splits);
-  return n * (D + 2) * 4;
+  const long splits = (cap + kSplit - 1) / kSplit;
+  return static_cast<long>(B) * Hq * Q * splits * (D + 2) * 4;
 }
 
 extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k,
