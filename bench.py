@@ -37,8 +37,22 @@ from hackthenorth_amd.kernels import rng as DR  # noqa: E402
 from hackthenorth_amd.model import Qwen3Model, shape_config  # noqa: E402
 
 METRIC = "batch-1 decode tok/s at Qwen3 shapes + per-kernel HBM GB/s as % of peak"
+# HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+# FETCH_SIZE / WRITE_SIZE passes (calibrated against a copy of known size).
+PMC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gateup_swiglu_qwen3-0.6b_pmc.txt")
 HBM_PEAK_GBS = 8000.0
 PROMPT_SEED, PROMPT_STREAM = 1, 7
+
+
+def measured_traffic():
+    try:
+        with open(PMC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def kv_bytes_per_token(cfg, ctx):
@@ -159,6 +173,39 @@ def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
             "affinity_cpus": len(os.sched_getaffinity(0))}
 
 
+def pmc_pass():
+    """Short, graph-free workload for rocprofv3 --pmc passes (counter collection
+    is per dispatch, so every kernel is launched eagerly): 8 decode steps of the
+    0.6B workload at context 512, 28 launches of the dominant kernel over the
+    layers' weights, and a 256 MiB device copy (reads and writes exactly 256 MiB)
+    that calibrates the byte counters."""
+    cfg = shape_config("qwen3-0.6b")
+    model = Qwen3Model.random(cfg)
+    cap = 512 + 8
+    with torch.inference_mode():
+        cache = D.KVCache(model, 1, cap)
+        rotary = D.RotaryTable(model, cap)
+        token = torch.zeros((1, 1), dtype=torch.int64, device=model.device)
+        for i in range(8):
+            pos = torch.tensor([512 + i], dtype=torch.int64, device=model.device)
+            token = D.forward(model, token, cache, pos, rotary=rotary)
+        x = torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16, device=model.device)
+        DR.normal_(x, 3, 99, 1.0)
+        gain = model.layers[0].post_attention_layernorm.weight
+        for layer in model.layers:
+            P.norm_projection(x, gain, layer.gate_up_weight, 1e-6, swiglu=True)
+        src = torch.empty(128 << 20, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        DR.normal_(src, 9, 9, 1.0)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    k, n2 = cfg.hidden_size, 2 * cfg.intermediate_size
+    print(json.dumps({"pmc_pass": True, "calibration_copy_bytes": src.numel() * 2,
+                      "dominant_kernel_bytes": n2 * k * 2 + k * 4 + cfg.intermediate_size * 2}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +215,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-8b", action="store_true")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="short workload for rocprofv3 counter passes (no JSON bench line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the batch-one decode path on exactly one GPU; "
@@ -176,6 +225,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         sys.exit(2)
+
+    if args.pmc_pass:
+        pmc_pass()
+        return
 
     def log(msg):
         if not args.quiet:
@@ -197,7 +250,7 @@ def main():
                    "batch": 1, "prompt_tokens": args.prompt, "decode_steps": args.steps},
         "roofline": {"bound": "hbm", "achieved": round(dom["achieved"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": dom["name"], "avg_launch_us": round(dom["avg_us"], 3),
                      "bytes_per_launch": dom["bytes"]},
         "decode_roofline": {"bytes_per_token": res["bytes_per_token"],
