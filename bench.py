@@ -135,6 +135,60 @@ def dominant_kernel(model, launches=280):
                 avg_us=avg_s * 1e6, bytes=algorithmic, achieved=achieved)
 
 
+def per_op_microbench(reps=10):
+    """Bandwidth of the row-wise fused ops at Qwen3-0.6B widths over 32768 rows
+    (bf16 activations N(0,1)): algorithmic bytes / average launch time."""
+    from hackthenorth_amd.kernels import embed as E
+    from hackthenorth_amd.kernels import fused as F
+    from hackthenorth_amd.kernels import rmsnorm as N
+    from hackthenorth_amd.model import Norm
+    rows, H, I, Hq, Hkv, Dh, V = 32768, 1024, 3072, 16, 8, 128, 151936
+    dev = torch.device("cuda")
+
+    def randn(shape, stream):
+        t = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        return DR.normal_(t, 11, stream, 1.0)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / 1e3 / reps
+
+    out = {}
+    x, r, g = randn((rows, H), 1), randn((rows, H), 2), randn((H,), 3)
+    t = timed(lambda: N.add_rms_norm(x, r, g, 1e-6))
+    out["add_rms_norm"] = (rows * H * 2 * 4 + H * 2, t, f"[{rows}, {H}]")
+    del x, r
+    gate, up = randn((rows, I), 4), randn((rows, I), 5)
+    t = timed(lambda: F.swiglu(gate, up))
+    out["swiglu"] = (rows * I * 2 * 3, t, f"[{rows}, {I}]")
+    del gate, up
+    packed = randn((1, rows, (Hq + 2 * Hkv) * Dh), 6)
+    q, k, v = (u.view(1, rows, -1, Dh) for u in packed.split((Hq * Dh, Hkv * Dh, Hkv * Dh), -1))
+    qn, kn = Norm(randn((Dh,), 7), 1e-6), Norm(randn((Dh,), 8), 1e-6)
+    cos, sin = (u.to(dev)[None] for u in D.rope_tables(shape_config("qwen3-0.6b"), rows))
+    keys = torch.zeros((1, Hkv, rows, Dh), dtype=torch.bfloat16, device=dev)
+    values = torch.zeros_like(keys)
+    positions = torch.arange(rows, device=dev)
+    t = timed(lambda: F.norm_rope_cache(q, k, v, qn, kn, cos, sin, keys, values, positions))
+    per_token = (Hq + 2 * Hkv) * Dh * 2 * 2 + 2 * Dh * 2 + 8
+    out["qk_norm_rope_kv_append"] = (rows * per_token, t, f"{rows} tokens x ({Hq} q + {Hkv} kv heads)")
+    del packed, keys, values
+    table = randn((V, H), 9)
+    ids = DR.randint(rows, V, 1, 8, device=dev)
+    t = timed(lambda: E.embed_gather(ids, table))
+    out["embed_gather"] = (rows * (H * 2 * 2 + 8), t, f"{rows} ids of [{V}, {H}]")
+    return {name: {"shape": shape, "bytes": b, "us": round(sec * 1e6, 2),
+                   "GBs": round(b / sec / 1e9, 1), "frac_of_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
+            for name, (b, sec, shape) in out.items()}
+
+
 def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
     from oracle import qwen3 as Q
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -260,6 +314,8 @@ def main():
         "first_tokens": [res["first"]] + res["tokens"][:15],
     }
     del res["model"]
+    torch.cuda.empty_cache()
+    line["per_op"] = per_op_microbench()
     torch.cuda.empty_cache()
     if not args.no_8b:
         try:

@@ -28,16 +28,56 @@ constexpr int kMergeUnroll = 8;     // partials loaded back to back in the merge
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
 //   n = bf16(g * bf16(x * inv)); out_i = bf16(bf16(n_i cos_i) + bf16(rot(n)_i sin_i)).
-__device__ __forceinline__ void norm_rope_wave(const bf16_t* x, const bf16_t* g, float eps,
-                                               const bf16_t* cs, const bf16_t* sn, int lane,
-                                               float& o0, float& o1) {
-  const float a = bf2f(x[lane]), b = bf2f(x[lane + 64]);
-  const float ss = wave_sum(a * a + b * b);
+// 16 lanes per 128-wide head: lane e owns elements 4e..4e+3 and their
+// rotate_half partners 64+4e..64+4e+3 (8-byte accesses), so RoPE needs no
+// cross-lane traffic and the sum of squares is one 16-lane DPP row sum. Every
+// kernel that normalises q or k uses these two functions, so the cache rows and
+// queries they produce are bit-identical.
+struct Head16 {
+  uint2 xa, xb, ga, gb, ca, cb, sa, sb;
+};
+
+__device__ __forceinline__ void head16_load(const bf16_t* x, const bf16_t* g, const bf16_t* cs,
+                                            const bf16_t* sn, int e, Head16& h) {
+  h.xa = *reinterpret_cast<const uint2*>(x + 4 * e);
+  h.xb = *reinterpret_cast<const uint2*>(x + 64 + 4 * e);
+  h.ga = *reinterpret_cast<const uint2*>(g + 4 * e);
+  h.gb = *reinterpret_cast<const uint2*>(g + 64 + 4 * e);
+  h.ca = *reinterpret_cast<const uint2*>(cs + 4 * e);
+  h.cb = *reinterpret_cast<const uint2*>(cs + 64 + 4 * e);
+  h.sa = *reinterpret_cast<const uint2*>(sn + 4 * e);
+  h.sb = *reinterpret_cast<const uint2*>(sn + 64 + 4 * e);
+}
+
+__device__ __forceinline__ void unpack4(uint2 v, float* o) {
+  o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
+}
+
+// All 64 lanes must call this (16-lane DPP reduction).
+__device__ __forceinline__ void head16_math(const Head16& h, float eps, uint2& oa, uint2& ob) {
+  float xa[4], xb[4], ga[4], gb[4], ca[4], cb[4], sa[4], sb[4];
+  unpack4(h.xa, xa); unpack4(h.xb, xb); unpack4(h.ga, ga); unpack4(h.gb, gb);
+  unpack4(h.ca, ca); unpack4(h.cb, cb); unpack4(h.sa, sa); unpack4(h.sb, sb);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss = fmaf(xa[i], xa[i], ss);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss = fmaf(xb[i], xb[i], ss);
+  ss = row16_sum(ss);
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-  const float na = round_bf(bf2f(g[lane]) * round_bf(a * inv));
-  const float nb = round_bf(bf2f(g[lane + 64]) * round_bf(b * inv));
-  o0 = round_bf(round_bf(na * bf2f(cs[lane])) + round_bf(-nb * bf2f(sn[lane])));
-  o1 = round_bf(round_bf(nb * bf2f(cs[lane + 64])) + round_bf(na * bf2f(sn[lane + 64])));
+  float na[4], nb[4], ra[4], rb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    na[i] = round_bf(ga[i] * round_bf(xa[i] * inv));
+    nb[i] = round_bf(gb[i] * round_bf(xb[i] * inv));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ra[i] = round_bf(round_bf(na[i] * ca[i]) + round_bf(-nb[i] * sa[i]));
+    rb[i] = round_bf(round_bf(nb[i] * cb[i]) + round_bf(na[i] * sb[i]));
+  }
+  oa = make_uint2(pack_bf2(ra[0], ra[1]), pack_bf2(ra[2], ra[3]));
+  ob = make_uint2(pack_bf2(rb[0], rb[1]), pack_bf2(rb[2], rb[3]));
 }
 
 struct RopeArgs {
@@ -53,11 +93,14 @@ struct RopeArgs {
 };
 
 __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, e = lane & 15;
   const long q_rows = static_cast<long>(a.B) * a.T * a.Hq;
   const long total = q_rows + static_cast<long>(a.B) * a.T * a.Hkv;
-  if (row >= total) return;
+  // Rows past the end recompute the last row (a whole 16-lane group must run
+  // the DPP reduction) and store nothing.
+  const long row_raw = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const bool live = row_raw < total;
+  const long row = live ? row_raw : total - 1;
   const bool is_q = row < q_rows;
   const long r = is_q ? row : row - q_rows;
   const int heads = is_q ? a.Hq : a.Hkv;
@@ -67,30 +110,34 @@ __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
   // Positions are only read when they select the rope row or the cache slot.
   const int64_t p = (a.rope_by_pos || a.keys) ? a.pos[t] : t;
   const long rr = a.rope_by_pos ? p : t;
-  if (rr < 0 || rr >= a.rope_rows) return;
-  const bf16_t* cs = a.cos + rr * a.rope_st;
-  const bf16_t* sn = a.sin + rr * a.rope_st;
-  float o0, o1;
+  const bool rope_ok = rr >= 0 && rr < a.rope_rows;
+  const long ri = rope_ok ? rr : 0;
+  const bf16_t* src = is_q ? a.q + b * a.q_sb + t * a.q_st + h * D
+                           : a.k + b * a.k_sb + t * a.k_st + h * D;
+  Head16 hd;
+  head16_load(src, is_q ? a.qg : a.kg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hd);
+  uint2 oa, ob;
+  head16_math(hd, is_q ? a.q_eps : a.k_eps, oa, ob);
+  if (!live || !rope_ok) return;
   if (is_q) {
-    norm_rope_wave(a.q + b * a.q_sb + t * a.q_st + h * D, a.qg, a.q_eps, cs, sn, lane, o0, o1);
     bf16_t* dst = a.out_q + ((b * a.T + t) * a.Hq + h) * D;
-    dst[lane] = static_cast<bf16_t>(f2bf(o0));
-    dst[lane + 64] = static_cast<bf16_t>(f2bf(o1));
+    *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
+    *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
     return;
   }
-  norm_rope_wave(a.k + b * a.k_sb + t * a.k_st + h * D, a.kg, a.k_eps, cs, sn, lane, o0, o1);
   if (a.out_k) {
     bf16_t* dst = a.out_k + ((b * a.T + t) * a.Hkv + h) * D;
-    dst[lane] = static_cast<bf16_t>(f2bf(o0));
-    dst[lane + 64] = static_cast<bf16_t>(f2bf(o1));
+    *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
+    *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
   }
   if (a.keys && p >= 0 && p < a.cap) {
     const long slot = ((b * a.Hkv + h) * a.cap + p) * D;
-    a.keys[slot + lane] = static_cast<bf16_t>(f2bf(o0));
-    a.keys[slot + lane + 64] = static_cast<bf16_t>(f2bf(o1));
+    *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+    *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
     const bf16_t* vs = a.v + b * a.v_sb + t * a.v_st + h * D;
-    a.values[slot + lane] = vs[lane];
-    a.values[slot + lane + 64] = vs[lane + 64];
+    *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = *reinterpret_cast<const uint2*>(vs + 4 * e);
+    *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) =
+        *reinterpret_cast<const uint2*>(vs + 64 + 4 * e);
   }
 }
 
@@ -109,49 +156,6 @@ struct AttnArgs {
   int B, Hq, Hkv, G, Q, splits, split;
   float scale;
 };
-
-// Per-head RMSNorm + RoPE for a 32-lane half wave: lane l of the half owns
-// elements l, l+32, l+64, l+96, i.e. the rotate_half pairs (l, l+64) and
-// (l+32, l+96). Loads are issued by norm_rope_load, math by norm_rope_math, so
-// a caller can put the loads ahead of its other memory traffic.
-struct HeadLoads {
-  float x[4], g[4], c[4], s[4];
-};
-
-__device__ __forceinline__ void norm_rope_load(const bf16_t* x, const bf16_t* g, const bf16_t* cs,
-                                               const bf16_t* sn, int hl, HeadLoads& h) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = hl + 32 * i;
-    h.x[i] = bf2f(x[e]);
-    h.g[i] = bf2f(g[e]);
-    h.c[i] = bf2f(cs[e]);
-    h.s[i] = bf2f(sn[e]);
-  }
-}
-
-// Sum over the 32 lanes of each half wave (lanes 0-31 and 32-63 separately).
-__device__ __forceinline__ float half_sum(float v, int lane) {
-  v = row16_sum(v);
-  const float lo = readlane(v, 0) + readlane(v, 16);
-  const float hi = readlane(v, 32) + readlane(v, 48);
-  return lane < 32 ? lo : hi;
-}
-
-__device__ __forceinline__ void norm_rope_math(const HeadLoads& h, float eps, int lane,
-                                               float (&o)[4]) {
-  const float ss =
-      half_sum((h.x[0] * h.x[0] + h.x[1] * h.x[1]) + (h.x[2] * h.x[2] + h.x[3] * h.x[3]), lane);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-  float n[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) n[i] = round_bf(h.g[i] * round_bf(h.x[i] * inv));
-  // element e < 64 pairs with e + 64 (rot = -n[e+64]); e >= 64 with e - 64 (rot = n[e-64])
-  o[0] = round_bf(round_bf(n[0] * h.c[0]) + round_bf(-n[2] * h.s[0]));
-  o[1] = round_bf(round_bf(n[1] * h.c[1]) + round_bf(-n[3] * h.s[1]));
-  o[2] = round_bf(round_bf(n[2] * h.c[2]) + round_bf(n[0] * h.s[2]));
-  o[3] = round_bf(round_bf(n[3] * h.c[3]) + round_bf(n[1] * h.s[3]));
-}
 
 // Split-KV partial attention for one (split of 64 slots, kv head, batch).
 // ROWS query rows (G heads x Q queries) are processed per chunk; K is read
@@ -191,23 +195,20 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   // ---- 1. prologue loads first (they gate the query rows), then K and V.
   // Every load is unconditional with its index clamped into valid memory:
   // loads under per-lane conditions serialise (one wait per load).
-  const int hl = lane & 31, half = lane >> 5;
-  const int head_slot = wave * 2 + half;  // 8 head slots per block: G query heads, then k
-  HeadLoads hq;
+  const int head_slot = wave * 4 + sub;  // 16 head slots per block: G query heads, then k
+  Head16 hq;
   const bf16_t* qrow = nullptr;
   bool do_head = false, is_k = false;
   if (FUSED) {
     const long rr = a.rope_by_pos ? newest : 0;
     const long ri = (rr >= 0 && rr < a.rope_rows) ? rr : 0;
-    const bf16_t* cs = a.cos + ri * a.rope_st;
-    const bf16_t* sn = a.sin + ri * a.rope_st;
     qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
     is_k = head_slot == a.G;
     do_head = head_slot < a.G || (is_k && has_newest);
     const int hs = head_slot < a.G ? head_slot : 0;
     const bf16_t* src = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
                              : qrow + (static_cast<long>(kvh) * a.G + hs) * D;
-    norm_rope_load(src, is_k ? a.kg : a.qg, cs, sn, hl, hq);
+    head16_load(src, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
   }
   uint4 kreg[4];
   uint32_t vreg[16];
@@ -228,24 +229,30 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
 
   // ---- 2. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
-    float o[4];
-    norm_rope_math(hq, is_k ? a.k_eps : a.q_eps, lane, o);
+    uint2 oa, ob;
+    head16_math(hq, is_k ? a.k_eps : a.q_eps, oa, ob);
     if (do_head && !is_k) {
+      float fa[4], fb[4];
+      unpack4(oa, fa);
+      unpack4(ob, fb);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qs[head_slot * D + hl + 32 * i] = o[i];
+      for (int i = 0; i < 4; ++i) {
+        qs[head_slot * D + 4 * e + i] = fa[i];
+        qs[head_slot * D + 64 + 4 * e + i] = fb[i];
+      }
     } else if (do_head) {
       const long slot = kv_base + newest * D;
       const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int el = hl + 32 * i;
-        const bf16_t kb = static_cast<bf16_t>(f2bf(o[i]));
-        const bf16_t vb = vsrc[el];
-        knew[el] = kb;
-        vnew[el] = vb;
-        a.keys[slot + el] = kb;
-        a.values[slot + el] = vb;
-      }
+      const uint2 va = *reinterpret_cast<const uint2*>(vsrc + 4 * e);
+      const uint2 vb = *reinterpret_cast<const uint2*>(vsrc + 64 + 4 * e);
+      *reinterpret_cast<uint2*>(knew + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(knew + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(vnew + 4 * e) = va;
+      *reinterpret_cast<uint2*>(vnew + 64 + 4 * e) = vb;
+      *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = va;
+      *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
     }
   } else {
     for (int i = tid; i < rows * D; i += kBlock) {
@@ -456,7 +463,7 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   const int rows = a.G * a.Q;
   if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
     return HTN_EUNSUPPORTED;
-  if (fused && a.G + 1 > 8) return HTN_EUNSUPPORTED;  // 8 head slots in the fused prologue
+  if (fused && a.G + 1 > 16) return HTN_EUNSUPPORTED;  // 16 head slots in the fused prologue
   a.split = kSplit;
   a.splits = static_cast<int>((a.cap + kSplit - 1) / kSplit);
   if (a.splits > 1 && !scratch) return HTN_EINVAL;
@@ -495,6 +502,11 @@ extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, co
   if ((rope_by_position || keys) && !positions) return HTN_EINVAL;
   if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || rope_rows <= 0) return HTN_EINVAL;
   if ((keys || values) && (!keys || !values || !v || cap <= 0)) return HTN_EINVAL;
+  // Heads are moved in 8-byte pieces: 4-element aligned rows only.
+  const void* ptrs[] = {q, k, v, q_gain, k_gain, cos, sin, keys, values, out_q, out_k};
+  for (const void* p : ptrs)
+    if (!aligned8(p)) return HTN_EUNSUPPORTED;
+  if ((q_sb | q_st | k_sb | k_st | rope_st | (v ? (v_sb | v_st) : 0)) & 3) return HTN_EUNSUPPORTED;
   RopeArgs a{};
   a.q = static_cast<const bf16_t*>(q); a.q_sb = q_sb; a.q_st = q_st;
   a.k = static_cast<const bf16_t*>(k); a.k_sb = k_sb; a.k_st = k_st;
@@ -509,7 +521,7 @@ extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, co
   a.B = static_cast<int>(B); a.T = static_cast<int>(T);
   a.Hq = static_cast<int>(Hq); a.Hkv = static_cast<int>(Hkv);
   const long total = B * T * (Hq + Hkv);
-  hipLaunchKernelGGL(norm_rope_cache_kernel, dim3((total + 3) / 4), dim3(kBlock), 0,
+  hipLaunchKernelGGL(norm_rope_cache_kernel, dim3((total + 15) / 16), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), a);
   return launch_status();
 }
@@ -521,6 +533,7 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
                                      htn_stream_t stream) {
   if (!q || !keys || !values || !positions || !out) return HTN_EINVAL;
   if (Hkv <= 0 || Hq % Hkv != 0 || Q <= 0) return HTN_EINVAL;
+  if (!aligned16(keys) || !aligned16(values)) return HTN_EUNSUPPORTED;
   AttnArgs a{};
   a.q = static_cast<const bf16_t*>(q); a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
   a.keys = static_cast<bf16_t*>(const_cast<void*>(keys));
@@ -542,6 +555,11 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
   if (!qkv || !q_gain || !k_gain || !cos || !sin || !keys || !values || !positions || !out)
     return HTN_EINVAL;
   if (Hkv <= 0 || groups <= 0 || rope_rows <= 0) return HTN_EINVAL;
+  const void* ptrs[] = {qkv, q_gain, k_gain, cos, sin};
+  for (const void* p : ptrs)
+    if (!aligned8(p)) return HTN_EUNSUPPORTED;
+  if ((qkv_sb | k_off | v_off | rope_st) & 3) return HTN_EUNSUPPORTED;
+  if (!aligned16(keys) || !aligned16(values)) return HTN_EUNSUPPORTED;
   AttnArgs a{};
   a.qkv = static_cast<const bf16_t*>(qkv); a.qkv_sb = qkv_sb; a.k_off = k_off; a.v_off = v_off;
   a.qg = static_cast<const bf16_t*>(q_gain); a.kg = static_cast<const bf16_t*>(k_gain);

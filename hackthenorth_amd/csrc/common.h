@@ -137,6 +137,7 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
 int device_cus();  // compute units of the current device (cached per device)
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 inline int launch_status() {
   return hipGetLastError() == hipSuccess ? HTN_OK : HTN_ELAUNCH;
