@@ -32,6 +32,8 @@ SIGNATURES = {
     "htn_version": [],
     "htn_fill_normal_bf16": [_P, _I64, _U64, _U64, _I64, _F, _P],
     "htn_fill_randint_i64": [_P, _I64, _U64, _U64, _I64, _P],
+    "htn_fill_uniform_f32": [_P, _I64, _U64, _U64, _F, _F, _P],
+    "htn_fill_weights_w8": [_P, _I64, _U64, _U64, _I, _P],
     "htn_embed_gather": [_P, _I64, _P, _I64, _I64, _P, _P],
     "htn_rms_norm": [_P, _I64, _P, _P, _I64, _I64, _F, _P],
     "htn_add_rms_norm": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
@@ -40,6 +42,10 @@ SIGNATURES = {
     "htn_gemv_norm": [_P, _P, _F, _P, _P, _I64, _I64, _I, _P],
     "htn_gemv_residual": [_P, _P, _P, _P, _I64, _I64, _P],
     "htn_lm_head_argmax": [_P, _P, _F, _P, _I64, _I64, _P, _P, _P, _P],
+    "htn_gemv_w8": [_P, _P, _P, _I, _P, _I64, _I64, _P],
+    "htn_gemv_norm_w8": [_P, _P, _F, _P, _P, _I, _P, _I64, _I64, _I, _P],
+    "htn_gemv_residual_w8": [_P, _P, _P, _I, _P, _P, _I64, _I64, _P],
+    "htn_lm_head_argmax_w8": [_P, _P, _F, _P, _P, _I, _I64, _I64, _P, _P, _P, _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],
     "htn_norm_rope_cache": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _F, _F,
                             _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _P, _P, _I64, _I64,

@@ -12,12 +12,77 @@
 //    reference) is staged once per block in LDS and read back with 16-byte
 //    LDS reads;
 //  * blocks grid-stride over row groups, so the prologue is paid once per
-//    block and the grid is sized to the CU count.
+//    block and the grid is sized to the CU count;
+//  * weight-only 8-bit variants (int8, fp8 e4m3fn) keep the same schedule with
+//    16 weights per 16-byte load and apply the per-output-channel fp32 scale
+//    to the fp32 dot product before the bf16 rounding.
 #include "common.h"
 
 namespace htn {
 
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+// Weight storage: bf16, or one byte per weight (int8 two's complement, or OCP
+// fp8 e4m3fn) with an fp32 scale per output row.
+enum WeightFormat { WF_BF16 = 0, WF_INT8 = HTN_WEIGHT_INT8, WF_FP8 = HTN_WEIGHT_FP8_E4M3 };
+
+template <int WF>
+struct Fmt {
+  static constexpr int kBytes = WF == WF_BF16 ? 2 : 1;  // bytes per weight
+  static constexpr int kPerVec = 16 / kBytes;           // weights per 16-byte load
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// acc + w.lo * x.lo + w.hi * x.hi for two packed bf16 pairs (v_dot2c_f32_bf16:
+// the bf16 products are exact in fp32, accumulation in fp32).
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                         __builtin_bit_cast(bf16x2_t, x), acc, false);
+}
+
+// Two fp32 values that are exact in bf16 (small integers) packed as bf16.
+__device__ __forceinline__ uint32_t pack_exact_bf2(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Partial dot product of one 16-byte weight vector with its activations,
+// which stay packed bf16 pairs (xp[i] holds activations 2i, 2i+1). Every
+// weight is first made an exact bf16 value, so each step is one bf16 dot2:
+//  bf16: 8 weights, used as loaded.
+//  int8: 16 weights; each byte converts to fp32 with sign extension in the
+//        conversion itself (exact), two values pack into one bf16 pair.
+//  fp8:  16 weights; the hardware converts two e4m3fn codes straight to a
+//        bf16 pair (gfx950 decodes OCP e4m3fn; every e4m3 value is a bf16
+//        value, and the unit scale leaves it unchanged).
+template <int WF>
+__device__ __forceinline__ float dot_vec(uint4 w, const uint32_t* xp, float s) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (WF == WF_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s = dot2(d[j], xp[j], s);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t p0, p1;
+      if constexpr (WF == WF_INT8) {
+        const int v = static_cast<int>(d[j]);
+        p0 = pack_exact_bf2(static_cast<float>(static_cast<signed char>(v)),
+                            static_cast<float>(static_cast<signed char>(v >> 8)));
+        p1 = pack_exact_bf2(static_cast<float>(static_cast<signed char>(v >> 16)),
+                            static_cast<float>(v >> 24));
+      } else {
+        p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                                              static_cast<int>(d[j]), 1.0f, false));
+        p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                                              static_cast<int>(d[j]), 1.0f, true));
+      }
+      s = dot2(p0, xp[2 * j], s);
+      s = dot2(p1, xp[2 * j + 1], s);
+    }
+  }
+  return s;
+}
 
 // LDS layout: [0, 64) argmax keys of the four waves, [64, 128) reduction
 // scratch, then the staged activation row.
@@ -26,7 +91,8 @@ constexpr int kLdsHead = 128;
 struct GemvArgs {
   const bf16_t* x;
   const bf16_t* gain;
-  const bf16_t* w;
+  const bf16_t* w;     // bf16 weights, or the bytes of an 8-bit format
+  const float* scale;  // 8-bit formats: one fp32 scale per weight row
   const bf16_t* res;
   bf16_t* y;
   int64_t* token_out;
@@ -80,19 +146,20 @@ __global__ __launch_bounds__(kBlock) void argmax_finish(const uint64_t* __restri
 // Weight batch: chunks c0 .. c0+U-1 of output rows n0 .. n0+R-1 (for SwiGLU
 // each is the pair gate row n, up row n + N). Lane l reads 16 bytes at vector
 // c*64 + l of each row; rows past the end re-read the last row (discarded).
-template <int R, int S, int U>
+template <int R, int S, int U, int WF>
 __device__ __forceinline__ void issue_batch(const GemvArgs& a, long n0, int c0, int kv, int lane,
                                             uint4 (&wv)[U][R][S]) {
+  const unsigned char* base = reinterpret_cast<const unsigned char*>(a.w);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const long n = n0 + r < a.n ? n0 + r : a.n - 1;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const bf16_t* row = a.w + (n + s * a.n) * static_cast<long>(a.k);
+      const unsigned char* row = base + (n + s * a.n) * static_cast<long>(a.k) * Fmt<WF>::kBytes;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int v = (c0 + u) * 64 + lane;
-        wv[u][r][s] = v < kv ? load_stream(row + v * 8) : make_uint4(0, 0, 0, 0);
+        wv[u][r][s] = v < kv ? load_stream(row + v * 16) : make_uint4(0, 0, 0, 0);
       }
     }
   }
@@ -103,14 +170,15 @@ __device__ __forceinline__ void issue_batch(const GemvArgs& a, long n0, int c0, 
 // without the RMSNorm prologue they are loaded next to each weight batch (L1
 // hits after the CU's first wave) and the waves never synchronise; with it the
 // block normalises x once into LDS, amortised over all rows the block streams.
-template <int R, int S, int U, bool NORM, int EPI>
+template <int R, int S, int U, bool NORM, int EPI, int WF>
 __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
+  constexpr int EPV = Fmt<WF>::kPerVec;  // weights (and activations) per lane per vector
   __shared__ uint64_t keys[kBlock / kWave];
   __shared__ float red[kBlock / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
   bf16_t* xs = reinterpret_cast<bf16_t*>(smem);   // normalised x (NORM only)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kv = a.k >> 3;
+  const int kv = a.k / EPV;
   const int chunks = (kv + 63) >> 6;
   const long groups = (a.n + R - 1) / R;
   const long stride = static_cast<long>(gridDim.x) * 4;
@@ -119,20 +187,21 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   // First weight batch before anything that waits on memory.
   uint4 wv[U][R][S];
   bool pending = grp < groups;
-  if (pending) issue_batch<R, S, U>(a, grp * R, 0, kv, lane, wv);
+  if (pending) issue_batch<R, S, U, WF>(a, grp * R, 0, kv, lane, wv);
 
   // RMSNorm prologue: the block normalises x once into LDS (bf16, rounded as
   // the reference rounds) and its waves then stream many rows against it.
   if constexpr (NORM) {
+    const int kv8 = a.k >> 3;
     float ss = 0.f;
-    for (int v = threadIdx.x; v < kv; v += kBlock) {
+    for (int v = threadIdx.x; v < kv8; v += kBlock) {
       float f[8];
       unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
     }
     const float inv = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(a.k) + a.eps);
-    for (int v = threadIdx.x; v < kv; v += kBlock) {
+    for (int v = threadIdx.x; v < kv8; v += kBlock) {
       float f[8], g[8];
       unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
       unpack8(*reinterpret_cast<const uint4*>(a.gain + v * 8), g);
@@ -155,33 +224,44 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
 #pragma unroll
       for (int s = 0; s < S; ++s) acc[r][s] = 0.f;
     for (int c0 = 0; c0 < chunks; c0 += U) {
-      if (!pending) issue_batch<R, S, U>(a, n0, c0, kv, lane, wv);
+      if (!pending) issue_batch<R, S, U, WF>(a, n0, c0, kv, lane, wv);
       pending = false;
-      uint4 xv[U];
+      uint4 xv[U][EPV / 8];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int v = (c0 + u) * 64 + lane;
-        if (NORM)
-          xv[u] = v < kv ? *reinterpret_cast<const uint4*>(xs + v * 8) : make_uint4(0, 0, 0, 0);
-        else
-          xv[u] = v < kv ? *reinterpret_cast<const uint4*>(a.x + v * 8) : make_uint4(0, 0, 0, 0);
+        const bf16_t* src = NORM ? xs : a.x;
+#pragma unroll
+        for (int h = 0; h < EPV / 8; ++h)
+          xv[u][h] = v < kv ? *reinterpret_cast<const uint4*>(src + v * EPV + 8 * h)
+                            : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        float xf[8];
-        unpack8(xv[u], xf);
+        uint32_t xp[EPV / 2];
+#pragma unroll
+        for (int h = 0; h < EPV / 8; ++h) {
+          xp[4 * h] = xv[u][h].x;
+          xp[4 * h + 1] = xv[u][h].y;
+          xp[4 * h + 2] = xv[u][h].z;
+          xp[4 * h + 3] = xv[u][h].w;
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int s = 0; s < S; ++s) acc[r][s] += dot8(wv[u][r][s], xf);
+          for (int s = 0; s < S; ++s) acc[r][s] = dot_vec<WF>(wv[u][r][s], xp, acc[r][s]);
       }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const long n = n0 + r;
-      const float t0 = wave_sum(acc[r][0]);
-      const float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
+      float t0 = wave_sum(acc[r][0]);
+      float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
       if (n < a.n) {
+        if (WF != WF_BF16) {
+          t0 *= a.scale[n];
+          if (S > 1) t1 *= a.scale[n + a.n];
+        }
         if (EPI == EPI_ARGMAX) {
           const uint64_t key = argmax_key(f2bf(t0), static_cast<uint32_t>(n));
           best = key > best ? key : best;
@@ -295,17 +375,20 @@ int finish_argmax(const GemvArgs& a, long blocks, hipStream_t st) {
 // Waves resident per CU at full occupancy of 4 blocks (16 waves).
 constexpr long kWavesPerCu = 16;
 
-template <int R, int S, int U, bool NORM, int EPI>
+template <int R, int S, int U, bool NORM, int EPI, int WF>
 int launch_vec(const GemvArgs& a, hipStream_t st) {
   const long groups = (a.n + R - 1) / R;
   // RMSNorm kernels pay their prologue once per block: when every wave would
   // stream three or more row groups anyway, two longer-lived blocks per CU
   // beat four. Kernels without a prologue fill the CU.
+  // 8-bit rows are half as long, so a wave holds half the bytes in flight:
+  // their norm kernels keep four blocks per CU (eight for 1 KB rows).
   long per_cu = 8;
-  if (NORM) per_cu = groups >= 3 * kWavesPerCu * device_cus() ? 2 : 4;
+  if (NORM && WF == WF_BF16) per_cu = groups >= 3 * kWavesPerCu * device_cus() ? 2 : 4;
+  if (NORM && WF != WF_BF16) per_cu = a.k > 1024 ? 4 : 8;
   const long blocks = grid_for(groups, per_cu);
   const size_t lds = NORM ? static_cast<size_t>(a.k) * 2 : 0;
-  hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI>), dim3(blocks), dim3(kBlock), lds, st, a);
+  hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI, WF>), dim3(blocks), dim3(kBlock), lds, st, a);
   if (EPI == EPI_ARGMAX) return finish_argmax(a, blocks, st);
   return launch_status();
 }
@@ -321,25 +404,47 @@ int launch_scalar(const GemvArgs& a, hipStream_t st) {
 
 // One output row (gate/up pair for SwiGLU) per wave by default, so even
 // 1024-row projections spread over every CU, with U 1 KB chunks per row in
-// flight. Short rows (K <= 1024) over many rows take four rows per wave so a
-// wave still keeps 8 KB of loads in flight.
-template <bool NORM, int EPI>
+// flight. Short rows (K <= 1024 bf16 weights) over many rows take four rows
+// per wave so a wave still keeps 8 KB of loads in flight. 8-bit weights need
+// 16-weight-aligned rows and have no scalar fallback.
+template <bool NORM, int EPI, int WF>
 int dispatch(GemvArgs& a, hipStream_t st) {
-  const bool vec = (a.k % 8 == 0) && aligned16(a.x) && aligned16(a.w) &&
+  constexpr int EPV = Fmt<WF>::kPerVec;
+  const bool vec = (a.k % EPV == 0) && aligned16(a.x) && aligned16(a.w) &&
                    (!NORM || aligned16(a.gain));
-  if (!vec) return launch_scalar<NORM, EPI>(a, st);
-  const int chunks = (a.k + 511) / 512;
+  if (!vec) {
+    if constexpr (WF == WF_BF16) return launch_scalar<NORM, EPI>(a, st);
+    else return HTN_EUNSUPPORTED;
+  }
+  const int chunks = (a.k / EPV + 63) / 64;
   constexpr int S = EPI == EPI_SWIGLU ? 2 : 1;
   const bool many_rows = a.n >= 4 * kWavesPerCu * device_cus();
-  if (chunks <= 2) {
-    if (S == 1 && many_rows) return launch_vec<4, S, 2, NORM, EPI>(a, st);
-    return launch_vec<1, S, 2, NORM, EPI>(a, st);
+  if (WF != WF_BF16) {
+    // 8-bit rows of one 1 KB chunk take one load per row, four rows per wave
+    // when there are rows enough; rows longer than 8 KB stream two at a time.
+    if (chunks == 1) {
+      if (S == 1 && many_rows) return launch_vec<4, S, 1, NORM, EPI, WF>(a, st);
+      return launch_vec<1, S, 1, NORM, EPI, WF>(a, st);
+    }
+    if (chunks > 8 && S == 1 && !NORM) return launch_vec<2, S, 8, NORM, EPI, WF>(a, st);
   }
-  if (chunks <= 4) return launch_vec<1, S, 4, NORM, EPI>(a, st);
-  return launch_vec<1, S, 8, NORM, EPI>(a, st);
+  if (chunks <= 2) {
+    if (S == 1 && many_rows) return launch_vec<4, S, 2, NORM, EPI, WF>(a, st);
+    return launch_vec<1, S, 2, NORM, EPI, WF>(a, st);
+  }
+  if (chunks <= 4) return launch_vec<1, S, 4, NORM, EPI, WF>(a, st);
+  return launch_vec<1, S, 8, NORM, EPI, WF>(a, st);
 }
 
 bool bad_sizes(int64_t n, int64_t k) { return n <= 0 || k <= 0 || k > kMaxK || n > (1L << 31); }
+
+bool bad_format(int format) { return format != WF_INT8 && format != WF_FP8; }
+
+// Runs dispatch<NORM, EPI, WF> for the runtime weight format.
+template <bool NORM, int EPI>
+int dispatch_w8(GemvArgs& a, int format, hipStream_t st) {
+  return format == WF_INT8 ? dispatch<NORM, EPI, WF_INT8>(a, st) : dispatch<NORM, EPI, WF_FP8>(a, st);
+}
 
 }  // namespace
 }  // namespace htn
@@ -355,7 +460,7 @@ extern "C" int htn_gemv(const void* x, const void* w, void* y, int64_t rows, int
   a.y = static_cast<bf16_t*>(y);
   a.n = rows;
   a.k = static_cast<int>(k);
-  return dispatch<false, EPI_STORE>(a, static_cast<hipStream_t>(stream));
+  return dispatch<false, EPI_STORE, WF_BF16>(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int htn_gemv_norm(const void* x, const void* gain, float eps, const void* w,
@@ -371,7 +476,7 @@ extern "C" int htn_gemv_norm(const void* x, const void* gain, float eps, const v
   a.k = static_cast<int>(k);
   a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return swiglu ? dispatch<true, EPI_SWIGLU>(a, st) : dispatch<true, EPI_STORE>(a, st);
+  return swiglu ? dispatch<true, EPI_SWIGLU, WF_BF16>(a, st) : dispatch<true, EPI_STORE, WF_BF16>(a, st);
 }
 
 extern "C" int htn_gemv_residual(const void* x, const void* w, const void* residual, void* y,
@@ -384,7 +489,7 @@ extern "C" int htn_gemv_residual(const void* x, const void* w, const void* resid
   a.y = static_cast<bf16_t*>(y);
   a.n = rows;
   a.k = static_cast<int>(k);
-  return dispatch<false, EPI_RESIDUAL>(a, static_cast<hipStream_t>(stream));
+  return dispatch<false, EPI_RESIDUAL, WF_BF16>(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
@@ -402,7 +507,77 @@ extern "C" int htn_lm_head_argmax(const void* x, const void* gain, float eps, co
   a.position_inc = position_inc;
   a.partial = static_cast<uint64_t*>(scratch);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return gain ? dispatch<true, EPI_ARGMAX>(a, st) : dispatch<false, EPI_ARGMAX>(a, st);
+  return gain ? dispatch<true, EPI_ARGMAX, WF_BF16>(a, st) : dispatch<false, EPI_ARGMAX, WF_BF16>(a, st);
+}
+
+extern "C" int htn_gemv_w8(const void* x, const void* w, const float* scales, int format,
+                           void* y, int64_t rows, int64_t k, htn_stream_t stream) {
+  if (!x || !w || !scales || !y || bad_sizes(rows, k) || bad_format(format)) return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.scale = scales;
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  return dispatch_w8<false, EPI_STORE>(a, format, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int htn_gemv_norm_w8(const void* x, const void* gain, float eps, const void* w,
+                                const float* scales, int format, void* y, int64_t rows,
+                                int64_t k, int swiglu, htn_stream_t stream) {
+  if (!x || !gain || !w || !scales || !y || bad_sizes(rows, k) || bad_format(format))
+    return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.gain = static_cast<const bf16_t*>(gain);
+  a.w = static_cast<const bf16_t*>(w);
+  a.scale = scales;
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return swiglu ? dispatch_w8<true, EPI_SWIGLU>(a, format, st)
+                : dispatch_w8<true, EPI_STORE>(a, format, st);
+}
+
+extern "C" int htn_gemv_residual_w8(const void* x, const void* w, const float* scales, int format,
+                                    const void* residual, void* y, int64_t rows, int64_t k,
+                                    htn_stream_t stream) {
+  if (!x || !w || !scales || !residual || !y || bad_sizes(rows, k) || bad_format(format))
+    return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.w = static_cast<const bf16_t*>(w);
+  a.scale = scales;
+  a.res = static_cast<const bf16_t*>(residual);
+  a.y = static_cast<bf16_t*>(y);
+  a.n = rows;
+  a.k = static_cast<int>(k);
+  return dispatch_w8<false, EPI_RESIDUAL>(a, format, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int htn_lm_head_argmax_w8(const void* x, const void* gain, float eps, const void* w,
+                                     const float* scales, int format, int64_t vocab, int64_t k,
+                                     int64_t* token_out, int64_t* position_inc, void* scratch,
+                                     htn_stream_t stream) {
+  if (!x || !w || !scales || !token_out || !scratch || bad_sizes(vocab, k) || bad_format(format))
+    return HTN_EINVAL;
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.gain = static_cast<const bf16_t*>(gain);
+  a.w = static_cast<const bf16_t*>(w);
+  a.scale = scales;
+  a.n = vocab;
+  a.k = static_cast<int>(k);
+  a.eps = eps;
+  a.token_out = token_out;
+  a.position_inc = position_inc;
+  a.partial = static_cast<uint64_t*>(scratch);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return gain ? dispatch_w8<true, EPI_ARGMAX>(a, format, st)
+              : dispatch_w8<false, EPI_ARGMAX>(a, format, st);
 }
 
 extern "C" int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,

@@ -65,9 +65,83 @@ __global__ __launch_bounds__(kBlock) void fill_randint(int64_t* __restrict__ out
   }
 }
 
+// lo + p with p already rounded: two roundings, as numpy performs them (the
+// pragma keeps the compiler from fusing the caller's multiply into an FMA).
+__device__ __forceinline__ float add_no_fma(float lo, float p) {
+#pragma clang fp contract(off)
+  return lo + p;
+}
+
+__global__ __launch_bounds__(kBlock) void fill_uniform(float* __restrict__ out, long count,
+                                                       uint64_t key, float lo, float span) {
+  for (long i = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < count;
+       i += static_cast<long>(gridDim.x) * kBlock) {
+    const uint64_t h = mix64(key + static_cast<uint64_t>(i + 1) * kGolden);
+    const float u = static_cast<float>(h >> 40) * (1.0f / 16777216.0f);  // exact
+    out[i] = add_no_fma(lo, span * u);
+  }
+}
+
+// Round-to-nearest-even fp8 e4m3fn encoding of a finite float with
+// |f| < 464 (larger magnitudes saturate to 448; only integers in [-127, 127]
+// are encoded here). Normals round the fp32 mantissa to 3 bits with the carry
+// running into the exponent; below 2^-6 the value is a multiple of 2^-9.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = fabsf(f);
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = static_cast<uint32_t>(rintf(a * 512.0f));  // 0..8; 8 is the smallest normal
+  } else {
+    const uint32_t au = __float_as_uint(a);
+    const uint32_t r = (au + 0x7ffffu + ((au >> 20) & 1u)) >> 20;  // (exp << 3) | mantissa
+    code = r - (120u << 3);
+    if (code > 0x7eu) code = 0x7eu;
+  }
+  return sign | code;
+}
+
+__global__ __launch_bounds__(kBlock) void fill_w8(uint8_t* __restrict__ out, long count,
+                                                  uint64_t key, int format) {
+  for (long i = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < count;
+       i += static_cast<long>(gridDim.x) * kBlock) {
+    const uint64_t h = mix64(key + static_cast<uint64_t>(i + 1) * kGolden);
+    const int v = static_cast<int>(((h >> 32) * 255u) >> 32) - 127;
+    out[i] = static_cast<uint8_t>(format == HTN_WEIGHT_INT8 ? static_cast<uint32_t>(v) & 0xffu
+                                                            : f32_to_e4m3(static_cast<float>(v)));
+  }
+}
+
+long fill_blocks(long count) {
+  long blocks = (count + kBlock - 1) / kBlock;
+  const long cap = static_cast<long>(device_cus()) * 16;
+  blocks = blocks < cap ? blocks : cap;
+  return blocks < 1 ? 1 : blocks;
+}
+
 }  // namespace htn
 
 using namespace htn;
+
+extern "C" int htn_fill_uniform_f32(float* out, int64_t count, uint64_t seed, uint64_t stream,
+                                    float lo, float span, htn_stream_t stream_) {
+  if (!out || count <= 0) return HTN_EINVAL;
+  hipLaunchKernelGGL(fill_uniform, dim3(fill_blocks(count)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream_), out, static_cast<long>(count),
+                     stream_key_host(seed, stream), lo, span);
+  return launch_status();
+}
+
+extern "C" int htn_fill_weights_w8(void* out, int64_t count, uint64_t seed, uint64_t stream,
+                                   int format, htn_stream_t stream_) {
+  if (!out || count <= 0 || (format != HTN_WEIGHT_INT8 && format != HTN_WEIGHT_FP8_E4M3))
+    return HTN_EINVAL;
+  hipLaunchKernelGGL(fill_w8, dim3(fill_blocks(count)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream_), static_cast<uint8_t*>(out),
+                     static_cast<long>(count), stream_key_host(seed, stream), format);
+  return launch_status();
+}
 
 extern "C" int htn_fill_normal_bf16(void* out, int64_t count, uint64_t seed, uint64_t stream,
                                     int64_t start, float scale, htn_stream_t stream_) {

@@ -5,19 +5,12 @@ to bf16 before adding the residual. Here one wave reduces a whole row (the
 grid already spans the CUs at these sizes), with the same two roundings:
 out = bf16(bf16(sum_k x_k w_nk) + residual_n).
 """
-import torch
-
-from .. import _lib
+from .projection import residual_projection
 
 
 def down_residual(x, w, residual):
+    """w may be a bf16 [H, I] tensor or a QuantizedWeight of that shape."""
     n, k = w.shape
     if x.numel() != k or residual.numel() != n:
         raise ValueError("down projection requires one activation and residual row")
-    if any(t.dtype != torch.bfloat16 or not t.is_contiguous() for t in (x, w, residual)):
-        raise ValueError("down projection requires contiguous BF16 tensors")
-    _lib.require_gpu(x, w, residual)
-    out = torch.empty_like(residual)
-    _lib.call("htn_gemv_residual", _lib.ptr(x), _lib.ptr(w), _lib.ptr(residual), _lib.ptr(out),
-              n, k, _lib.stream(x.device))
-    return out
+    return residual_projection(x, w, residual, "down projection")

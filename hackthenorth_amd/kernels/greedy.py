@@ -8,6 +8,7 @@ advances the position) in place on the device.
 import torch
 
 from .. import _lib
+from ..quant import QuantizedWeight
 
 
 def greedy_head(x, gain, eps, w, out, advance=None):
@@ -21,8 +22,14 @@ def greedy_head(x, gain, eps, w, out, advance=None):
         raise ValueError("greedy head expects one contiguous row and a row-major weight")
     if out.dtype != torch.int64 or (advance is not None and advance.dtype != torch.int64):
         raise ValueError("token and position buffers must be int64")
-    _lib.require_gpu(x, w, out)
     scratch = torch.empty(_lib.HEAD_SCRATCH_BYTES, dtype=torch.uint8, device=x.device)
+    if isinstance(w, QuantizedWeight):
+        _lib.require_gpu(x, w.data, out)
+        _lib.call("htn_lm_head_argmax_w8", _lib.ptr(x), _lib.ptr(gain), float(eps),
+                  _lib.ptr(w.data), _lib.ptr(w.scale), w.code, w.shape[0], k, _lib.ptr(out),
+                  _lib.ptr(advance), _lib.ptr(scratch), _lib.stream(x.device))
+        return out
+    _lib.require_gpu(x, w, out)
     _lib.call("htn_lm_head_argmax", _lib.ptr(x), _lib.ptr(gain), float(eps), _lib.ptr(w),
               w.shape[0], k, _lib.ptr(out), _lib.ptr(advance), _lib.ptr(scratch),
               _lib.stream(x.device))

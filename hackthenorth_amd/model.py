@@ -15,6 +15,10 @@ layouts without transformers:
 Weights come either from a checkpoint directory (config.json + *.safetensors
 with the Hugging Face tensor names) or, for the synthetic benchmark shapes,
 from a seeded device-side generator (config.json carrying "random_init").
+
+With weight_format "int8" or "fp8_e4m3" the four projections of every layer
+and the LM head are QuantizedWeight objects (one byte per weight plus an fp32
+scale per row); the embedding table and the norm gains stay bf16.
 """
 import glob
 import json
@@ -24,16 +28,23 @@ from dataclasses import dataclass, field, asdict
 import torch
 
 from .kernels import rng
+from .quant import FORMATS, QuantizedWeight
 
 # Generator stream ids per tensor; the test oracle regenerates the same
 # weights from the same ids and seed.
 STREAM_EMBED = 1
 STREAM_LM_HEAD = 2
+STREAM_LM_HEAD_SCALE = 3
 _LAYER_KINDS = {"qkv": 0, "o": 1, "gate_up": 2, "down": 3}
+SCALE_STREAM_OFFSET = 8  # 8-bit weights: row scales of a tensor use its stream + 8
 
 
 def layer_stream(layer, kind):
     return 100 + 16 * layer + _LAYER_KINDS[kind]
+
+
+def _nbytes(t):
+    return t.nbytes() if isinstance(t, QuantizedWeight) else t.numel() * t.element_size()
 
 
 @dataclass
@@ -49,6 +60,7 @@ class Qwen3Config:
     rms_norm_eps: float = 1e-6
     rope_theta: float = 1e6
     random_init: dict = field(default=None)
+    weight_format: str = "bf16"   # or "int8" / "fp8_e4m3" (weight-only, per-row scales)
 
     @classmethod
     def from_dict(cls, d):
@@ -62,6 +74,12 @@ class Qwen3Config:
 
     def to_dict(self):
         return {k: v for k, v in asdict(self).items() if v is not None}
+
+    @property
+    def quantized(self):
+        if self.weight_format != "bf16" and self.weight_format not in FORMATS:
+            raise ValueError(f"unknown weight_format {self.weight_format!r}")
+        return self.weight_format != "bf16"
 
     @property
     def widths(self):
@@ -108,10 +126,16 @@ class Layer:
         d = c.head_dim
         opts = dict(dtype=torch.bfloat16, device=device)
         self.layer_idx = index
-        self.qkv_weight = torch.empty((sum(c.widths), c.hidden_size), **opts)
-        self.o_weight = torch.empty((c.hidden_size, c.num_attention_heads * d), **opts)
-        self.gate_up_weight = torch.empty((2 * c.intermediate_size, c.hidden_size), **opts)
-        self.down_weight = torch.empty((c.hidden_size, c.intermediate_size), **opts)
+
+        def weight(rows, cols):
+            if c.quantized:
+                return QuantizedWeight.empty(rows, cols, c.weight_format, device)
+            return torch.empty((rows, cols), **opts)
+
+        self.qkv_weight = weight(sum(c.widths), c.hidden_size)
+        self.o_weight = weight(c.hidden_size, c.num_attention_heads * d)
+        self.gate_up_weight = weight(2 * c.intermediate_size, c.hidden_size)
+        self.down_weight = weight(c.hidden_size, c.intermediate_size)
         self.input_layernorm = Norm(torch.ones(c.hidden_size, **opts), c.rms_norm_eps)
         self.post_attention_layernorm = Norm(torch.ones(c.hidden_size, **opts), c.rms_norm_eps)
         self.q_norm = Norm(torch.ones(d, **opts), c.rms_norm_eps)
@@ -134,8 +158,13 @@ class Qwen3Model:
         opts = dict(dtype=torch.bfloat16, device=self.device)
         c = config
         self.embed_weight = torch.empty((c.vocab_size, c.hidden_size), **opts)
-        self.lm_head_weight = (self.embed_weight if c.tie_word_embeddings
-                               else torch.empty((c.vocab_size, c.hidden_size), **opts))
+        if c.quantized:
+            # The LM head streams 8-bit rows; the gather table stays bf16 even when tied.
+            self.lm_head_weight = QuantizedWeight.empty(c.vocab_size, c.hidden_size,
+                                                        c.weight_format, self.device)
+        else:
+            self.lm_head_weight = (self.embed_weight if c.tie_word_embeddings
+                                   else torch.empty((c.vocab_size, c.hidden_size), **opts))
         self.norm = Norm(torch.ones(c.hidden_size, **opts), c.rms_norm_eps)
         self.layers = [Layer(c, i, self.device) for i in range(c.num_hidden_layers)]
 
@@ -147,31 +176,42 @@ class Qwen3Model:
         """Bytes of all weight tensors resident in HBM."""
         total = self.embed_weight.numel() * 2
         if self.lm_head_weight is not self.embed_weight:
-            total += self.lm_head_weight.numel() * 2
+            total += _nbytes(self.lm_head_weight)
         for layer in self.layers:
-            total += sum(t.numel() * 2 for t in layer.tensors().values())
+            total += sum(_nbytes(t) for t in layer.tensors().values())
         return total
 
     def decode_weight_bytes(self):
         """Weight bytes one decode step must read: every projection and the LM
         head once, plus the single embedding row and the norm gains."""
         c = self.config
-        total = self.lm_head_weight.numel() * 2 + c.hidden_size * 2 * 2
+        total = _nbytes(self.lm_head_weight) + c.hidden_size * 2 * 2
         for layer in self.layers:
-            total += sum(t.numel() * 2 for t in layer.tensors().values())
+            total += sum(_nbytes(t) for t in layer.tensors().values())
             total += (2 * c.hidden_size + 2 * c.head_dim) * 2
         return total
 
     # ------------------------------------------------------------------ init
 
     def randomize(self, seed=0, std=0.02):
-        """Fill every projection with the seeded device generator; gains stay 1."""
+        """Fill every projection with the seeded device generator; gains stay 1.
+
+        bf16: N(0, std). 8-bit formats: uniform integers in [-127, 127] (fp8:
+        their e4m3fn rounding) with row scales U(0.001, 0.01); the embedding
+        table is N(0, std) bf16 either way.
+        """
         rng.normal_(self.embed_weight, seed, STREAM_EMBED, std)
-        if self.lm_head_weight is not self.embed_weight:
+        if isinstance(self.lm_head_weight, QuantizedWeight):
+            self.lm_head_weight.randomize_(seed, STREAM_LM_HEAD, STREAM_LM_HEAD_SCALE)
+        elif self.lm_head_weight is not self.embed_weight:
             rng.normal_(self.lm_head_weight, seed, STREAM_LM_HEAD, std)
         for i, layer in enumerate(self.layers):
             for kind, t in layer.tensors().items():
-                rng.normal_(t, seed, layer_stream(i, kind), std)
+                st = layer_stream(i, kind)
+                if isinstance(t, QuantizedWeight):
+                    t.randomize_(seed, st, st + SCALE_STREAM_OFFSET)
+                else:
+                    rng.normal_(t, seed, st, std)
         return self
 
     @classmethod
@@ -179,21 +219,21 @@ class Qwen3Model:
         return cls(config, device).randomize(seed, std)
 
     def load_state(self, tensors):
-        """Copy Hugging Face-named tensors into the packed layouts."""
-        c = self.config
+        """Copy Hugging Face-named tensors into the packed layouts (8-bit formats:
+        quantized per row on the way in)."""
         with torch.no_grad():
             self.embed_weight.copy_(tensors["model.embed_tokens.weight"])
             if self.lm_head_weight is not self.embed_weight:
-                self.lm_head_weight.copy_(tensors["lm_head.weight"])
+                _assign(self.lm_head_weight, tensors["lm_head.weight"])
             self.norm.weight.copy_(tensors["model.norm.weight"])
             for i, layer in enumerate(self.layers):
                 p = f"model.layers.{i}."
-                layer.qkv_weight.copy_(torch.cat([tensors[p + f"self_attn.{n}_proj.weight"]
-                                                  for n in ("q", "k", "v")]))
-                layer.o_weight.copy_(tensors[p + "self_attn.o_proj.weight"])
-                layer.gate_up_weight.copy_(torch.cat([tensors[p + f"mlp.{n}_proj.weight"]
-                                                      for n in ("gate", "up")]))
-                layer.down_weight.copy_(tensors[p + "mlp.down_proj.weight"])
+                _assign(layer.qkv_weight, torch.cat([tensors[p + f"self_attn.{n}_proj.weight"]
+                                                     for n in ("q", "k", "v")]))
+                _assign(layer.o_weight, tensors[p + "self_attn.o_proj.weight"])
+                _assign(layer.gate_up_weight, torch.cat([tensors[p + f"mlp.{n}_proj.weight"]
+                                                         for n in ("gate", "up")]))
+                _assign(layer.down_weight, tensors[p + "mlp.down_proj.weight"])
                 layer.input_layernorm.weight.copy_(tensors[p + "input_layernorm.weight"])
                 layer.post_attention_layernorm.weight.copy_(
                     tensors[p + "post_attention_layernorm.weight"])
@@ -224,9 +264,19 @@ class Qwen3Model:
         raise FileNotFoundError(f"{model_path}: no *.safetensors and no random_init in config.json")
 
 
-def write_random_model_dir(path, shape="qwen3-0.6b", seed=0, std=0.02):
+def _assign(dst, src):
+    if isinstance(dst, QuantizedWeight):
+        q = QuantizedWeight.quantize(src.to(dst.device), dst.format)
+        dst.data.copy_(q.data)
+        dst.scale.copy_(q.scale)
+    else:
+        dst.copy_(src)
+
+
+def write_random_model_dir(path, shape="qwen3-0.6b", seed=0, std=0.02, weight_format="bf16"):
     """Write a checkpoint directory whose weights are regenerated from the seed."""
     os.makedirs(path, exist_ok=True)
     with open(os.path.join(path, "config.json"), "w") as f:
-        json.dump(shape_config(shape, seed, std).to_dict(), f, indent=1)
+        json.dump(shape_config(shape, seed, std, weight_format=weight_format).to_dict(), f,
+                  indent=1)
     return path

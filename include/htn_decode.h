@@ -36,6 +36,11 @@ extern "C" {
 #define HTN_HEAD_SCRATCH_BYTES 65536
 #define HTN_HEAD_DIM 128
 
+/* 8-bit weight formats of the *_w8 GEMVs (one byte per weight, row-major,
+ * one fp32 scale per weight row). */
+#define HTN_WEIGHT_INT8 1     /* two's complement int8 */
+#define HTN_WEIGHT_FP8_E4M3 2 /* OCP fp8 e4m3fn (bias 7, no infinities, 0x7f/0xff NaN) */
+
 typedef void* htn_stream_t;
 
 /* Library version, for the loader's sanity check. */
@@ -52,6 +57,20 @@ int htn_fill_normal_bf16(void* out, int64_t count, uint64_t seed, uint64_t strea
 /* out[i] = floor((hash >> 32) * high / 2^32) as int64. */
 int htn_fill_randint_i64(int64_t* out, int64_t count, uint64_t seed, uint64_t stream,
                          int64_t high, htn_stream_t stream_);
+
+/* out[i] = lo + span * (f32(hash >> 40) * 2^-24), each operation rounded
+ * once in fp32 (synthetic per-channel weight scales, lo = 0.001 and span =
+ * 0.009 for U(0.001, 0.01)). No reference counterpart: the 8-bit weight
+ * variants are an addition to the reference's bf16-only decode path. */
+int htn_fill_uniform_f32(float* out, int64_t count, uint64_t seed, uint64_t stream, float lo,
+                         float span, htn_stream_t stream_);
+
+/* Synthetic 8-bit weights: v = floor((hash >> 32) * 255 / 2^32) - 127, a
+ * uniform integer in [-127, 127], stored as int8 (format HTN_WEIGHT_INT8) or
+ * as its round-to-nearest-even fp8 e4m3fn encoding (HTN_WEIGHT_FP8_E4M3).
+ * No reference counterpart (see htn_fill_uniform_f32). */
+int htn_fill_weights_w8(void* out, int64_t count, uint64_t seed, uint64_t stream, int format,
+                        htn_stream_t stream_);
 
 /* ---------------------------------------------------------------- gather */
 
@@ -112,6 +131,31 @@ int htn_gemv_residual(const void* x, const void* w, const void* residual, void* 
 int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w,
                        int64_t vocab, int64_t k, int64_t* token_out,
                        int64_t* position_inc, void* scratch, htn_stream_t stream);
+
+/* ---------------------------------------------------------------- 8-bit weights
+ * Weight-only 8-bit twins of the four GEMVs above: w holds rows*k bytes in
+ * `format` (HTN_WEIGHT_*), scales[n] is the fp32 scale of weight row n
+ * (gate/up: 2*rows scales, gate rows first). Every dot product is
+ *   y[n] = s_n * sum_k x[k] * w[n, k]   (fp32 accumulate, then the scale),
+ * rounded to bf16 where the bf16 GEMV rounds its plain dot product, so the
+ * norm prologue and the SwiGLU / residual / argmax epilogues keep the same
+ * rounding boundaries. k must be a multiple of 16 and x, gain and w 16-byte
+ * aligned (HTN_EUNSUPPORTED otherwise).
+ * No reference counterpart: dryft decodes in bf16 only; these cover the
+ * int8 / fp8 weight-only decode of the same projections (QKV, O, gate/up,
+ * down, LM head). */
+int htn_gemv_w8(const void* x, const void* w, const float* scales, int format, void* y,
+                int64_t rows, int64_t k, htn_stream_t stream);
+int htn_gemv_norm_w8(const void* x, const void* gain, float eps, const void* w,
+                     const float* scales, int format, void* y, int64_t rows, int64_t k,
+                     int swiglu, htn_stream_t stream);
+int htn_gemv_residual_w8(const void* x, const void* w, const float* scales, int format,
+                         const void* residual, void* y, int64_t rows, int64_t k,
+                         htn_stream_t stream);
+int htn_lm_head_argmax_w8(const void* x, const void* gain, float eps, const void* w,
+                          const float* scales, int format, int64_t vocab, int64_t k,
+                          int64_t* token_out, int64_t* position_inc, void* scratch,
+                          htn_stream_t stream);
 
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,

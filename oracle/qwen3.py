@@ -33,6 +33,16 @@ boundaries the reference kernels keep:
   greedy head       dryft/engine/kernels/greedy.py:27-29,41 and decode.py:99 --
                     logits rounded to bf16, argmax with the lowest id on ties.
 
+8-bit weight-only variants (no reference counterpart: dryft decodes in bf16)
+replace every projection and the LM head by y = bf16(s_n * sum_k x_k w_nk)
+with exact int8 / fp8-e4m3fn weight values and fp32 row scales s_n; all other
+roundings are unchanged.
+
+The 8-bit linear is pinned in tests/test_oracle.py: with unit scales it
+equals the bf16 linear of the same (bf16-exact) weight values, a scale
+multiplies the output before the rounding (checked against a hand example),
+and the generator's codes decode to the integer draws.
+
 Parity pinned: tests/test_oracle.py checks this module against the installed
 transformers Qwen3 implementation on identical weights (same formulas as
 4.51.3), against hand-computed known answers copied from the reference tests
@@ -83,6 +93,9 @@ SHAPES = {
 # same ids so both sides regenerate identical weights from one seed.
 STREAM_EMBED = 1
 STREAM_LM_HEAD = 2
+STREAM_LM_HEAD_SCALE = 3
+SCALE_STREAM_OFFSET = 8
+W8_FORMATS = ("int8", "fp8_e4m3")
 
 
 def layer_stream(layer, kind):
@@ -98,19 +111,46 @@ def normal_bf16(seed, stream, shape, std):
     return bf16_from_bits(rng.normal_bf16_bits(seed, stream, count, std), shape)
 
 
-def generate_weights(shape, seed=0, std=0.02):
-    """Random-init weights N(0, std) (Irwin-Hall approximation), gains 1."""
+def w8_weight(seed, stream, scale_stream, shape, fmt):
+    """(exact float32 weight values, float32 row scales U(0.001, 0.01))."""
+    count = int(np.prod(shape))
+    codes = rng.w8_codes(seed, stream, count, fmt)
+    values = torch.from_numpy(rng.w8_values(codes, fmt)).reshape(shape)
+    scale = torch.from_numpy(rng.uniform_f32(seed, scale_stream, shape[0], 0.001, 0.01))
+    return values, scale
+
+
+def generate_weights(shape, seed=0, std=0.02, weight_format="bf16"):
+    """Random-init weights N(0, std) (Irwin-Hall approximation), gains 1.
+
+    weight_format "int8" / "fp8_e4m3": the projections and the LM head are
+    uniform integers in [-127, 127] (fp8: their e4m3fn rounding) held as exact
+    float32 values, with row scales under "<name>.scale"; the embedding table
+    stays N(0, std) bf16.
+    """
     s = shape
     w = {"embed": normal_bf16(seed, STREAM_EMBED, (s.vocab, s.hidden), std)}
-    w["lm_head"] = w["embed"] if s.tied else normal_bf16(
-        seed, STREAM_LM_HEAD, (s.vocab, s.hidden), std)
+    if weight_format not in W8_FORMATS + ("bf16",):
+        raise ValueError(weight_format)
+
+    def put(name, stream, dims, scale_stream=None):
+        if weight_format == "bf16":
+            w[name] = normal_bf16(seed, stream, dims, std)
+            return
+        if scale_stream is None:
+            scale_stream = stream + SCALE_STREAM_OFFSET
+        w[name], w[name + ".scale"] = w8_weight(seed, stream, scale_stream, dims, weight_format)
+
+    if s.tied and weight_format == "bf16":
+        w["lm_head"] = w["embed"]
+    else:
+        put("lm_head", STREAM_LM_HEAD, (s.vocab, s.hidden), STREAM_LM_HEAD_SCALE)
     w["norm"] = torch.ones(s.hidden, dtype=BF16)
     for l in range(s.layers):
-        w[f"{l}.qkv"] = normal_bf16(seed, layer_stream(l, "qkv"), (s.qkv_rows, s.hidden), std)
-        w[f"{l}.o"] = normal_bf16(seed, layer_stream(l, "o"),
-                                  (s.hidden, s.q_heads * s.head_dim), std)
-        w[f"{l}.gate_up"] = normal_bf16(seed, layer_stream(l, "gate_up"), (2 * s.ffn, s.hidden), std)
-        w[f"{l}.down"] = normal_bf16(seed, layer_stream(l, "down"), (s.hidden, s.ffn), std)
+        put(f"{l}.qkv", layer_stream(l, "qkv"), (s.qkv_rows, s.hidden))
+        put(f"{l}.o", layer_stream(l, "o"), (s.hidden, s.q_heads * s.head_dim))
+        put(f"{l}.gate_up", layer_stream(l, "gate_up"), (2 * s.ffn, s.hidden))
+        put(f"{l}.down", layer_stream(l, "down"), (s.hidden, s.ffn))
         for g in ("ln1", "ln2"):
             w[f"{l}.{g}"] = torch.ones(s.hidden, dtype=BF16)
         for g in ("q_norm", "k_norm"):
@@ -136,6 +176,11 @@ def add_rms_norm(x, residual, gain, eps):
 def linear(x, weight):
     """bf16(sum fp32(x * w)) -- dryft/engine/kernels/projection.py:25."""
     return (x.float() @ weight.float().T).to(BF16)
+
+
+def linear_w8(x, values, scale):
+    """bf16(s_n * sum fp32(x * w)) for exact 8-bit weight values and fp32 row scales."""
+    return ((x.float() @ values.float().T) * scale.float()).to(BF16)
 
 
 def silu_mul(gate, up):
@@ -225,8 +270,14 @@ class Oracle:
         # fp32 copies of the bf16 weights: products of bf16 are exact in fp32.
         self.f32 = {k: v.float() for k, v in self.weights.items() if v.dim() == 2}
 
+    def _dot(self, x, name):
+        """fp32 dot products, times the row scales of an 8-bit weight."""
+        y = x.float() @ self.f32[name].T
+        scale = self.weights.get(name + ".scale")
+        return y if scale is None else y * scale
+
     def _linear(self, x, name):
-        return (x.float() @ self.f32[name].T).to(BF16)
+        return self._dot(x, name).to(BF16)
 
     def layer(self, l, h, cache, positions):
         """Decoder layer l on hidden rows h [B, T, H] at absolute `positions`.
@@ -270,7 +321,7 @@ class Oracle:
             if record is not None:
                 record.append(h.clone())
         x = rms_norm(h[:, -1:] if last_only else h, w["norm"], s.eps)
-        logits = x.float() @ self.f32["lm_head"].T
+        logits = self._dot(x, "lm_head")
         logits_bf16 = logits.to(BF16)
         return greedy(logits_bf16), logits, logits_bf16
 

@@ -19,9 +19,13 @@ Distributions:
                 N(0, std^2) that stays bit-reproducible.
   randint(n)    multiply-shift of the top 32 bits: floor(u32 * n / 2^32).
   uniform(a,b)  a + (b-a) * (top 24 bits / 2^24), fp32 multiply then add.
+  w8 codes      randint(255) - 127 as int8 bytes, or the round-to-nearest-even
+                OCP fp8 e4m3fn encoding of that integer.
 
 Parity pinned: tests/test_oracle_rng.py checks the moments, the range
-limits, and hand-computed splitmix64 values for known counters.
+limits, and hand-computed splitmix64 values for known counters; the e4m3fn
+encoder and decoder are checked against torch.float8_e4m3fn conversions over
+every code and over all integers in [-127, 127].
 """
 import numpy as np
 
@@ -120,3 +124,57 @@ def int8_uniform(seed, stream, count, start=0):
     with np.errstate(over="ignore"):
         v = ((h >> np.uint64(32)) * np.uint64(255)) >> np.uint64(32)
     return (v.astype(np.int64) - 127).astype(np.int8)
+
+
+def int8_codes(seed, stream, count, start=0):
+    """int8_uniform as raw two's complement bytes (uint8)."""
+    return int8_uniform(seed, stream, count, start).view(np.uint8)
+
+
+def e4m3_decode(codes):
+    """OCP fp8 e4m3fn codes (uint8) -> float32: sign, 4-bit exponent with bias 7,
+    3-bit mantissa; exponent 0 is subnormal (m * 2^-9); 0x7f / 0xff are NaN."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c >> 7, -1.0, 1.0)
+    e = (c >> 3) & 15
+    m = c & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (8 + m) * np.exp2(e - 10.0))
+    out = (sign * mag).astype(np.float32)
+    out[(e == 15) & (m == 7)] = np.nan
+    return out
+
+
+def e4m3_encode(x):
+    """float32 -> e4m3fn codes with round-to-nearest-even; |x| >= 464 saturates
+    to 448 (the generator never reaches it). Exact for every value the grid
+    holds; other values go to the nearer grid neighbour, ties to even mantissa."""
+    x = np.asarray(x, dtype=np.float32)
+    grid = e4m3_decode(np.arange(0x7f, dtype=np.uint8)).astype(np.float64)  # 0 .. 448
+    a = np.abs(x).astype(np.float64)
+    hi = np.clip(np.searchsorted(grid, a, side="left"), 0, len(grid) - 1)
+    lo = np.clip(hi - 1, 0, len(grid) - 1)
+    d_lo = a - grid[lo]
+    d_hi = grid[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo)
+    code = np.where(a >= grid[-1], 0x7e, code)
+    sign = (np.signbit(x) & (code != 0)).astype(np.int64) << 7
+    return (code | sign).astype(np.uint8)
+
+
+def w8_codes(seed, stream, count, fmt, start=0):
+    """Synthetic 8-bit weight bytes: uniform integers in [-127, 127] stored as
+    int8 ("int8") or as their e4m3fn encoding ("fp8_e4m3")."""
+    v = int8_uniform(seed, stream, count, start)
+    if fmt == "int8":
+        return v.view(np.uint8)
+    if fmt == "fp8_e4m3":
+        return e4m3_encode(v.astype(np.float32))
+    raise ValueError(fmt)
+
+
+def w8_values(codes, fmt):
+    """Exact float32 values of 8-bit weight codes."""
+    if fmt == "int8":
+        return np.asarray(codes, dtype=np.uint8).view(np.int8).astype(np.float32)
+    return e4m3_decode(codes)

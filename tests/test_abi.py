@@ -15,10 +15,22 @@ def declared():
     return sorted(set(re.findall(r"\b(?:int|int64_t)\s+(htn_\w+)\s*\(", text)))
 
 
+def declared_arity():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(?:int|int64_t)\s+(htn_\w+)\s*\(([^)]*)\)", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
 def test_header_and_binding_agree():
     names = declared()
     assert names, "no entry points parsed from the header"
     assert sorted(_lib.SIGNATURES) == names
+    arity = declared_arity()
+    for name, args in _lib.SIGNATURES.items():
+        assert len(args) == arity[name], name
 
 
 def test_library_exports_every_declared_symbol():
@@ -37,3 +49,8 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.htn_embed_gather(None, 1, null, 10, 8, null, null) == _lib.HTN_EINVAL
     assert lib.htn_attention_scratch_bytes(1, 16, 1, 575) > 0
     assert lib.htn_attention_scratch_bytes(0, 16, 1, 575) == 0
+    # 8-bit GEMVs reject unknown formats and missing scales.
+    one = ctypes.c_void_p(256)
+    assert lib.htn_gemv_w8(one, one, one, 3, one, 16, 16, null) == _lib.HTN_EINVAL
+    assert lib.htn_gemv_w8(one, one, null, 1, one, 16, 16, null) == _lib.HTN_EINVAL
+    assert lib.htn_fill_weights_w8(one, 16, 0, 0, 0, null) == _lib.HTN_EINVAL
