@@ -192,6 +192,28 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   const int64_t newest = FUSED ? qp[0] : -1;
   const bool has_newest = FUSED && active && newest >= start && newest < end;
 
+  // Splits past the last position: neutral partials (max -inf, sum 0) and no
+  // loads. Returning here keeps every load below unconditional, so the
+  // compiler's wait counts stay exact (a branch that joins with fewer loads
+  // in flight makes it wait for all of them).
+  if (!active) {  // block-uniform
+    for (int i = tid; i < rows * D; i += kBlock) {
+      const int r = i / D, d = i % D;
+      const int h = kvh * a.G + r / a.Q, t = r % a.Q;
+      const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
+      if (a.splits == 1) {
+        a.out[orow * D + d] = static_cast<bf16_t>(f2bf(__builtin_nanf("")));
+      } else {
+        a.part[(orow * a.splits + s) * D + d] = 0.f;
+        if (d == 0) {
+          a.ml[(orow * a.splits + s) * 2] = -INFINITY;
+          a.ml[(orow * a.splits + s) * 2 + 1] = 0.f;
+        }
+      }
+    }
+    return;
+  }
+
   // ---- 1. prologue loads first (they gate the query rows), then K and V.
   // Every load is unconditional with its index clamped into valid memory:
   // loads under per-lane conditions serialise (one wait per load).
@@ -212,19 +234,17 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   }
   uint4 kreg[4];
   uint32_t vreg[16];
-  if (active) {  // block-uniform
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      long j = start + u * 16 + wave * 4 + sub;
-      j = j < end ? j : end - 1;
-      kreg[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
-    }
+  for (int u = 0; u < 4; ++u) {
+    long j = start + u * 16 + wave * 4 + sub;
+    j = j < end ? j : end - 1;
+    kreg[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
+  }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      long j = start + wave * 16 + i;
-      j = j < end ? j : end - 1;
-      vreg[i] = *reinterpret_cast<const uint32_t*>(a.values + kv_base + j * D + 2 * lane);
-    }
+  for (int i = 0; i < 16; ++i) {
+    long j = start + wave * 16 + i;
+    j = j < end ? j : end - 1;
+    vreg[i] = *reinterpret_cast<const uint32_t*>(a.values + kv_base + j * D + 2 * lane);
   }
 
   // ---- 2. query rows (and, fused, the newest k/v) into LDS
@@ -284,69 +304,59 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
     }
   }
 
-  const int len = active ? static_cast<int>(end - start) : 0;
+  const int len = static_cast<int>(end - start);
   for (int r0 = 0; r0 < rows; r0 += ROWS) {
     float acc[ROWS][2];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.f;
-    if (active) {
-      // ---- 3. scores q.k * D^-1/2 (rows past `rows` compute on zeros, never stored)
-      float qr[ROWS][8];
-      int64_t rp[ROWS];
+    // ---- 3. scores q.k * D^-1/2 (rows past `rows` compute on zeros, never stored)
+    float qr[ROWS][8];
+    int64_t rp[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const bool ok = r0 + r < rows;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qr[r][i] = ok ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
+      rp[r] = -1;
+#pragma unroll
+      for (int t = 0; t < kMaxQ; ++t)
+        if (ok && t == (r0 + r) % a.Q) rp[r] = qp[t];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long j = start + u * 16 + wave * 4 + sub;
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
-        const bool ok = r0 + r < rows;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qr[r][i] = ok ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
-        rp[r] = -1;
-#pragma unroll
-        for (int t = 0; t < kMaxQ; ++t)
-          if (ok && t == (r0 + r) % a.Q) rp[r] = qp[t];
+        const float dsum = row16_sum(dot8(kreg[u], qr[r]));
+        if (e == 0 && j < end) sc[r * kSplit + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
       }
+    }
+    __syncthreads();
+    // ---- 4. exact softmax numerators per row over this split
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const long j = start + u * 16 + wave * 4 + sub;
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-          const float dsum = row16_sum(dot8(kreg[u], qr[r]));
-          if (e == 0 && j < end) sc[r * kSplit + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
-        }
+    for (int r = wave; r < ROWS; r += 4) {
+      const float v = lane < len ? sc[r * kSplit + lane] : -INFINITY;
+      const float m = wave_max(v);
+      const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
+      sc[r * kSplit + lane] = p;
+      const float l = wave_sum(p);
+      if (lane == 0) {
+        mrow[r] = m;
+        lrow[r] = l;
       }
-      __syncthreads();
-      // ---- 4. exact softmax numerators per row over this split
+    }
+    __syncthreads();
+    // ---- 5. P.V: wave w owns slots w*16 .. w*16+15 of the split, each lane 2 dims;
+    // slots past the end carry p = 0 and a clamped (finite) V row.
 #pragma unroll
-      for (int r = wave; r < ROWS; r += 4) {
-        const float v = lane < len ? sc[r * kSplit + lane] : -INFINITY;
-        const float m = wave_max(v);
-        const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
-        sc[r * kSplit + lane] = p;
-        const float l = wave_sum(p);
-        if (lane == 0) {
-          mrow[r] = m;
-          lrow[r] = l;
-        }
-      }
-      __syncthreads();
-      // ---- 5. P.V: wave w owns slots w*16 .. w*16+15 of the split, each lane 2 dims;
-      // slots past the end carry p = 0 and a clamped (finite) V row.
+    for (int i = 0; i < 16; ++i) {
+      const int js = wave * 16 + i;
+      const float v0 = bf_lo(vreg[i]), v1 = bf_hi(vreg[i]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int js = wave * 16 + i;
-        const float v0 = bf_lo(vreg[i]), v1 = bf_hi(vreg[i]);
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-          const float p = sc[r * kSplit + js];
-          acc[r][0] = fmaf(p, v0, acc[r][0]);
-          acc[r][1] = fmaf(p, v1, acc[r][1]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = wave; r < ROWS; r += 4) {
-        if (lane == 0) {
-          mrow[r] = -INFINITY;
-          lrow[r] = 0.f;
-        }
+      for (int r = 0; r < ROWS; ++r) {
+        const float p = sc[r * kSplit + js];
+        acc[r][0] = fmaf(p, v0, acc[r][0]);
+        acc[r][1] = fmaf(p, v1, acc[r][1]);
       }
     }
 #pragma unroll
