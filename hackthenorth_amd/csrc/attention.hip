@@ -157,18 +157,35 @@ struct AttnArgs {
   float scale;
 };
 
+// Query source of the partial kernel: q rows from memory, or the fused
+// prologue over the packed projection row with the RoPE row either already
+// selected (row 0 of cos/sin) or looked up by the device position.
+enum Prologue { PRO_NONE = 0, PRO_ROW = 1, PRO_BY_POSITION = 2 };
+
 // Split-KV partial attention for one (split of 64 slots, kv head, batch).
 // ROWS query rows (G heads x Q queries) are processed per chunk; K is read
-// with 16 lanes per 256-byte row (dot products finish with DPP row sums), V
-// with one wave per 16 slots and 4 bytes per lane (P.V needs no cross-lane
-// reduction). Splits past the last position write neutral partials
-// (max -inf, sum 0) so the merge never needs the positions.
-template <int ROWS, bool FUSED>
+// with 16 lanes per 256-byte row (q.k as bf16 dot2 steps finishing with DPP
+// row sums), V with one wave per 16 slots and 4 bytes per lane (P.V needs no
+// cross-lane reduction). K and V are read through buffer descriptors over the
+// (batch, kv head) cache rows: slots past the capacity read as zeros, so the
+// tile loads need no per-lane clamping. Splits past the last position write
+// neutral partials (max -inf, sum 0) so the merge never needs the positions.
+//
+// Load order matters: vector loads complete in issue order, so a wait for one
+// load waits for every load issued before it. The small loads that gate the
+// query rows go first (unless their address needs the device position), then
+// K, then V; positions are scalar loads on their own counter. Every load is
+// unconditional: a branch that joins with fewer loads in flight, or a load
+// under a per-lane condition, makes the compiler wait for all of them.
+template <int ROWS, int PRO>
 __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
-  __shared__ float qs[kMaxRows * D];
+  constexpr bool FUSED = PRO != PRO_NONE;
+  constexpr int kQLoads = kMaxRows * (D / 2) / kBlock;  // q pairs per thread, unfused
+  __shared__ uint32_t qs[kMaxRows * D / 2];  // query rows as bf16 pairs
   __shared__ float sc[ROWS * kSplit];
   __shared__ float accr[4 * ROWS * D];
   __shared__ float mrow[ROWS], lrow[ROWS];
+  __shared__ long rowpos[kMaxRows];  // absolute position of each query row
   __shared__ __align__(16) bf16_t knew[D];
   __shared__ __align__(16) bf16_t vnew[D];
 
@@ -177,89 +194,82 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int rows = a.G * a.Q;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
+  const long start = static_cast<long>(s) * kSplit;
 
+  // ---- 1. loads that gate the query rows.
+  // Fused: 16 lanes per head slot, slots 0..G-1 the query heads, slot G the
+  // new key (its value is copied at step 3).
+  const int head_slot = wave * 4 + sub;
+  const bool is_k = head_slot == a.G;
+  const bf16_t* qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
+  const bf16_t* hsrc = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
+                            : qrow + (static_cast<long>(kvh) * a.G +
+                                      (head_slot < a.G ? head_slot : 0)) * D;
+  Head16 hq;
+  if (PRO == PRO_ROW) head16_load(hsrc, is_k ? a.kg : a.qg, a.cos, a.sin, e, hq);
+  // Unfused: the q rows (bf16 pairs) and each row's position, clamped reads.
+  uint32_t qv[kQLoads];
+  long rpv = 0;
+  if (!FUSED) {
+#pragma unroll
+    for (int i = 0; i < kQLoads; ++i) {
+      const int idx = tid + i * kBlock;
+      const int c = idx < rows * (D / 2) ? idx : 0;
+      const int r = c / (D / 2), d = 2 * (c % (D / 2));
+      const int h = kvh * a.G + r / a.Q, t = r % a.Q;
+      qv[i] = *reinterpret_cast<const uint32_t*>(
+          a.q + static_cast<long>(b) * a.q_sb + static_cast<long>(h) * a.q_sh +
+          static_cast<long>(t) * a.q_st + d);
+    }
+    rpv = a.pos[(tid < rows ? tid : 0) % a.Q];
+  }
+
+  // ---- 2. the split's K then V tiles (addresses from the block index only).
+  // Slots past the last position are masked below (scores -inf, V zeroed),
+  // so splits past it produce neutral partials with no branch.
+  const uint32_t row_bytes = static_cast<uint32_t>(a.cap) * D * 2;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base, row_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base, row_bytes);
+  uint4 kreg[4];
+  uint32_t vreg[16];
+  const uint32_t koff = static_cast<uint32_t>(((start + wave * 4 + sub) * D + e * 8) * 2);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) kreg[u] = buffer_load16(krs, koff, u * 16 * D * 2);
+  const uint32_t voff = static_cast<uint32_t>(((start + wave * 16) * D + 2 * lane) * 2);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) vreg[i] = buffer_load4(vrs, voff + i * D * 2, 0);
+
+  // Positions: scalar loads of pos[min(t, Q - 1)] (in bounds, branch-free).
   int64_t qp[kMaxQ];
   int64_t maxpos = -1;
 #pragma unroll
   for (int t = 0; t < kMaxQ; ++t) {
-    qp[t] = t < a.Q ? a.pos[t] : -1;
+    const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+    qp[t] = t < a.Q ? v : -1;
     maxpos = qp[t] > maxpos ? qp[t] : maxpos;
   }
   if (maxpos >= a.cap) maxpos = a.cap - 1;
-  const long start = static_cast<long>(s) * kSplit;
   const long end = start + kSplit < maxpos + 1 ? start + kSplit : maxpos + 1;
   const bool active = start <= maxpos;
   const int64_t newest = FUSED ? qp[0] : -1;
   const bool has_newest = FUSED && active && newest >= start && newest < end;
-
-  // Splits past the last position: neutral partials (max -inf, sum 0) and no
-  // loads. Returning here keeps every load below unconditional, so the
-  // compiler's wait counts stay exact (a branch that joins with fewer loads
-  // in flight makes it wait for all of them).
-  if (!active) {  // block-uniform
-    for (int i = tid; i < rows * D; i += kBlock) {
-      const int r = i / D, d = i % D;
-      const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-      const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
-      if (a.splits == 1) {
-        a.out[orow * D + d] = static_cast<bf16_t>(f2bf(__builtin_nanf("")));
-      } else {
-        a.part[(orow * a.splits + s) * D + d] = 0.f;
-        if (d == 0) {
-          a.ml[(orow * a.splits + s) * 2] = -INFINITY;
-          a.ml[(orow * a.splits + s) * 2 + 1] = 0.f;
-        }
-      }
-    }
-    return;
+  if (PRO == PRO_BY_POSITION) {
+    // The RoPE row needs the position: these loads queue behind K and V.
+    const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
+    head16_load(hsrc, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
   }
 
-  // ---- 1. prologue loads first (they gate the query rows), then K and V.
-  // Every load is unconditional with its index clamped into valid memory:
-  // loads under per-lane conditions serialise (one wait per load).
-  const int head_slot = wave * 4 + sub;  // 16 head slots per block: G query heads, then k
-  Head16 hq;
-  const bf16_t* qrow = nullptr;
-  bool do_head = false, is_k = false;
+  // ---- 3. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
-    const long rr = a.rope_by_pos ? newest : 0;
-    const long ri = (rr >= 0 && rr < a.rope_rows) ? rr : 0;
-    qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
-    is_k = head_slot == a.G;
-    do_head = head_slot < a.G || (is_k && has_newest);
-    const int hs = head_slot < a.G ? head_slot : 0;
-    const bf16_t* src = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
-                             : qrow + (static_cast<long>(kvh) * a.G + hs) * D;
-    head16_load(src, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
-  }
-  uint4 kreg[4];
-  uint32_t vreg[16];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    long j = start + u * 16 + wave * 4 + sub;
-    j = j < end ? j : end - 1;
-    kreg[u] = *reinterpret_cast<const uint4*>(a.keys + kv_base + j * D + e * 8);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    long j = start + wave * 16 + i;
-    j = j < end ? j : end - 1;
-    vreg[i] = *reinterpret_cast<const uint32_t*>(a.values + kv_base + j * D + 2 * lane);
-  }
-
-  // ---- 2. query rows (and, fused, the newest k/v) into LDS
-  if (FUSED) {
+    const bool do_head = head_slot < a.G || (is_k && has_newest);
     uint2 oa, ob;
     head16_math(hq, is_k ? a.k_eps : a.q_eps, oa, ob);
+    if (tid < a.G) rowpos[tid] = newest;
     if (do_head && !is_k) {
-      float fa[4], fb[4];
-      unpack4(oa, fa);
-      unpack4(ob, fb);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qs[head_slot * D + 4 * e + i] = fa[i];
-        qs[head_slot * D + 64 + 4 * e + i] = fb[i];
-      }
+      qs[head_slot * (D / 2) + 2 * e] = oa.x;
+      qs[head_slot * (D / 2) + 2 * e + 1] = oa.y;
+      qs[head_slot * (D / 2) + 32 + 2 * e] = ob.x;
+      qs[head_slot * (D / 2) + 32 + 2 * e + 1] = ob.y;
     } else if (do_head) {
       const long slot = kv_base + newest * D;
       const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
@@ -275,23 +285,19 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
     }
   } else {
-    for (int i = tid; i < rows * D; i += kBlock) {
-      const int r = i / D, d = i % D;
-      const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-      qs[i] = bf2f(a.q[static_cast<long>(b) * a.q_sb + static_cast<long>(h) * a.q_sh +
-                       static_cast<long>(t) * a.q_st + d]);
-    }
+    if (tid < rows) rowpos[tid] = rpv;
+#pragma unroll
+    for (int i = 0; i < kQLoads; ++i)
+      if (tid + i * kBlock < rows * (D / 2)) qs[tid + i * kBlock] = qv[i];
   }
   __syncthreads();
   if (has_newest) {  // block-uniform: the newest slot's k/v come from LDS, not memory
     const uint4 kn = *reinterpret_cast<const uint4*>(knew + e * 8);
     const uint32_t vn = *reinterpret_cast<const uint32_t*>(vnew + 2 * lane);
-    // Match on the clamped index: lanes past the end loaded slot end - 1,
-    // which is the newest slot itself.
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const long j = start + u * 16 + wave * 4 + sub;
-      const bool hit = (j < end ? j : end - 1) == newest;
+      const bool hit = j == newest;
       kreg[u].x = hit ? kn.x : kreg[u].x;
       kreg[u].y = hit ? kn.y : kreg[u].y;
       kreg[u].z = hit ? kn.z : kreg[u].z;
@@ -300,39 +306,40 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const long j = start + wave * 16 + i;
-      vreg[i] = (j < end ? j : end - 1) == newest ? vn : vreg[i];
+      vreg[i] = j == newest ? vn : vreg[i];
     }
   }
 
-  const int len = static_cast<int>(end - start);
+  const int len = active ? static_cast<int>(end - start) : 0;
   for (int r0 = 0; r0 < rows; r0 += ROWS) {
     float acc[ROWS][2];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.f;
-    // ---- 3. scores q.k * D^-1/2 (rows past `rows` compute on zeros, never stored)
-    float qr[ROWS][8];
-    int64_t rp[ROWS];
+    // ---- 4. scores q.k * D^-1/2. Rows past `rows` (when ROWS does not
+    // divide it) compute on whatever their LDS rows hold and are never stored.
+    uint32_t qr[ROWS][4];
+    long rp[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-      const bool ok = r0 + r < rows;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qr[r][i] = ok ? qs[(r0 + r) * D + e * 8 + i] : 0.f;
-      rp[r] = -1;
-#pragma unroll
-      for (int t = 0; t < kMaxQ; ++t)
-        if (ok && t == (r0 + r) % a.Q) rp[r] = qp[t];
+      for (int i = 0; i < 4; ++i) qr[r][i] = qs[(r0 + r) * (D / 2) + e * 4 + i];
+      rp[r] = rowpos[r0 + r];
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const long j = start + u * 16 + wave * 4 + sub;
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
-        const float dsum = row16_sum(dot8(kreg[u], qr[r]));
+        float dot = dot2(kreg[u].x, qr[r][0], 0.f);
+        dot = dot2(kreg[u].y, qr[r][1], dot);
+        dot = dot2(kreg[u].z, qr[r][2], dot);
+        dot = dot2(kreg[u].w, qr[r][3], dot);
+        const float dsum = row16_sum(dot);
         if (e == 0 && j < end) sc[r * kSplit + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
       }
     }
     __syncthreads();
-    // ---- 4. exact softmax numerators per row over this split
+    // ---- 5. exact softmax numerators per row over this split
 #pragma unroll
     for (int r = wave; r < ROWS; r += 4) {
       const float v = lane < len ? sc[r * kSplit + lane] : -INFINITY;
@@ -346,12 +353,14 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       }
     }
     __syncthreads();
-    // ---- 5. P.V: wave w owns slots w*16 .. w*16+15 of the split, each lane 2 dims;
-    // slots past the end carry p = 0 and a clamped (finite) V row.
+    // ---- 6. P.V: wave w owns slots w*16 .. w*16+15 of the split, each lane 2 dims;
+    // slots past the end carry p = 0 and a zeroed V row (the cache may hold
+    // anything there, NaN included).
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int js = wave * 16 + i;
-      const float v0 = bf_lo(vreg[i]), v1 = bf_hi(vreg[i]);
+      const uint32_t vv = js < len ? vreg[i] : 0u;
+      const float v0 = bf_lo(vv), v1 = bf_hi(vv);
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
         const float p = sc[r * kSplit + js];
@@ -463,16 +472,20 @@ namespace {
 template <int ROWS>
 void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.splits, a.Hkv, a.B);
-  if (fused)
-    hipLaunchKernelGGL((attention_partial<ROWS, true>), grid, dim3(kBlock), 0, st, a);
+  if (!fused)
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_NONE>), grid, dim3(kBlock), 0, st, a);
+  else if (a.rope_by_pos)
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_BY_POSITION>), grid, dim3(kBlock), 0, st, a);
   else
-    hipLaunchKernelGGL((attention_partial<ROWS, false>), grid, dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_ROW>), grid, dim3(kBlock), 0, st, a);
 }
 
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   const int rows = a.G * a.Q;
   if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
     return HTN_EUNSUPPORTED;
+  // One (batch, kv head) cache row is addressed with 32-bit byte offsets.
+  if (a.cap > (1L << 31) / (D * 2) - kSplit) return HTN_EUNSUPPORTED;
   if (fused && a.G + 1 > 16) return HTN_EUNSUPPORTED;  // 16 head slots in the fused prologue
   a.split = kSplit;
   a.splits = static_cast<int>((a.cap + kSplit - 1) / kSplit);
@@ -544,6 +557,8 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
   if (!q || !keys || !values || !positions || !out) return HTN_EINVAL;
   if (Hkv <= 0 || Hq % Hkv != 0 || Q <= 0) return HTN_EINVAL;
   if (!aligned16(keys) || !aligned16(values)) return HTN_EUNSUPPORTED;
+  // Query rows are read as bf16 pairs.
+  if ((reinterpret_cast<uintptr_t>(q) & 3u) || ((q_sb | q_sh | q_st) & 1)) return HTN_EUNSUPPORTED;
   AttnArgs a{};
   a.q = static_cast<const bf16_t*>(q); a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
   a.keys = static_cast<bf16_t*>(const_cast<void*>(keys));

@@ -32,15 +32,6 @@ struct Fmt {
   static constexpr int kPerVec = 16 / kBytes;           // weights per 16-byte load
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// acc + w.lo * x.lo + w.hi * x.hi for two packed bf16 pairs (v_dot2c_f32_bf16:
-// the bf16 products are exact in fp32, accumulation in fp32).
-__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
-                                         __builtin_bit_cast(bf16x2_t, x), acc, false);
-}
-
 // Two fp32 values that are exact in bf16 (small integers) packed as bf16.
 __device__ __forceinline__ uint32_t pack_exact_bf2(float lo, float hi) {
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);

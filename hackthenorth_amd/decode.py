@@ -15,7 +15,8 @@ advances the position.
 """
 import torch
 
-from .kernels.attention import decode_attention, grouped_attention
+from ._lib import HEAD_DIM
+from .kernels.attention import decode_attention, grouped_attention, prologue_attention
 from .kernels.down import down_residual
 from .kernels.embed import embed_gather
 from .kernels.fused import norm_rope_cache
@@ -67,23 +68,33 @@ class RotaryTable:
     """Prompt-independent RoPE rows for every cache slot, resident on the device.
 
     `tables` is (cos, sin), each [1, capacity, 128], as the reference's table
-    (decode.py:55-62); `select` gathers rows by device positions. The decode
-    step reads the row for the device position inside the attention kernel.
+    (decode.py:55-62); `select` gathers rows by device positions. `rows` holds
+    the same values as one [capacity, 256] table (cos | sin per slot), so the
+    decode step gathers its row with a single launch and every layer's
+    attention reads it at a fixed address.
     """
 
     def __init__(self, model, capacity, enabled=True):
         cos, sin = rope_tables(model.config, capacity)
         self.tables = (cos[None].to(model.device), sin[None].to(model.device))
+        self.rows = torch.cat((cos, sin), dim=-1).to(model.device).contiguous()
+
+    def step_row(self, position):
+        """(cos, sin) rows [1, 128] for the device position, one gather launch."""
+        row = embed_gather(position.reshape(1), self.rows)
+        return row[:, :HEAD_DIM], row[:, HEAD_DIM:]
 
     def select(self, positions):
         return tuple(t.index_select(1, positions) for t in self.tables)
 
 
-def decode_layer(model, i, h, cache, position, rotary):
+def decode_layer(model, i, h, cache, position, rotary, rope=None):
     """Decoder layer i for one token at batch one: five kernels, h [1, H] -> [1, H].
 
-    Appends the layer's K/V at the device `position` and reads the RoPE row
-    for it from the rotary table inside the attention kernel.
+    Appends the layer's K/V at the device `position`. `rope`, the step's
+    (cos, sin) rows from RotaryTable.step_row, lets the attention kernel load
+    them without waiting for the position; without it the kernel looks the
+    row up in the rotary table by position.
     """
     c = model.config
     layer = model.layers[i]
@@ -92,9 +103,14 @@ def decode_layer(model, i, h, cache, position, rotary):
     cos, sin = rotary.tables
     ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
     packed = norm_projection(h, ln1.weight, layer.qkv_weight, ln1.variance_epsilon)
-    a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
-                         cache.keys[i], cache.values[i], position,
-                         c.num_key_value_heads, groups, q_width, q_width + k_width)
+    if rope is not None:
+        a = prologue_attention(packed, layer.q_norm, layer.k_norm, rope[0], rope[1],
+                               cache.keys[i], cache.values[i], position,
+                               c.num_key_value_heads, groups, q_width, q_width + k_width)
+    else:
+        a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
+                             cache.keys[i], cache.values[i], position,
+                             c.num_key_value_heads, groups, q_width, q_width + k_width)
     r = output_projection_residual(a, layer.o_weight, h)
     m = norm_projection(r, ln2.weight, layer.gate_up_weight, ln2.variance_epsilon,
                         swiglu=True)
@@ -106,8 +122,9 @@ def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=Non
 
     `record`, when a list, receives the hidden state after every layer."""
     h = embed_gather(token_ids.reshape(1), model.embed_weight)
+    rope = rotary.step_row(position)
     for i in range(len(model.layers)):
-        h = decode_layer(model, i, h, cache, position, rotary)
+        h = decode_layer(model, i, h, cache, position, rotary, rope)
         if record is not None:
             record.append(h)
     if out is None:
