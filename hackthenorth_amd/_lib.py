@@ -46,6 +46,9 @@ SIGNATURES = {
     "htn_gemv_norm_w8": [_P, _P, _F, _P, _P, _I, _P, _I64, _I64, _I, _P],
     "htn_gemv_residual_w8": [_P, _P, _P, _I, _P, _P, _I64, _I64, _P],
     "htn_lm_head_argmax_w8": [_P, _P, _F, _P, _P, _I, _I64, _I64, _P, _P, _P, _P],
+    "htn_gemm_rows_scratch_bytes": [_I64, _I64, _I64, _I],
+    "htn_gemm_rows": [_P, _I64, _P, _F, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P,
+                      _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],
     "htn_norm_rope_cache": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _F, _F,
                             _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _P, _P, _I64, _I64,
@@ -56,7 +59,8 @@ SIGNATURES = {
     "htn_prologue_attention": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64, _I,
                                _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P],
 }
-RESTYPES = {"htn_attention_scratch_bytes": _I64}
+RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64}
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3
 
 _lib = None
 _lock = threading.Lock()

@@ -1,0 +1,328 @@
+// Multi-row projections for the speculative verify pass (2 to 32 rows).
+//
+// y[m, n] = sum_k x[m, k] W[n, k] for every row m < M with the weight read
+// once for all rows: the rows form the A operand of gfx950's
+// v_mfma_f32_16x16x32_bf16 (one or two 16-row tiles, rows past M are zero),
+// a strip of 16 weight rows the B operand. The kernel stays HBM-bound on W:
+//
+//  * block = 4 waves on one 16-column strip (plus the matching up strip for
+//    SwiGLU); the waves take interleaved 32-wide k steps of the block's K
+//    range, each lane loading 16 contiguous bytes of one weight row per step,
+//    U steps in flight;
+//  * when the strips alone cannot fill the GPU, K is split over KS blocks
+//    whose fp32 partials a second, stream-ordered launch sums in a fixed
+//    order (deterministic) before the epilogue;
+//  * the optional RMSNorm prologue computes each row's 1/rms once per block
+//    and normalises x fragments as they are loaded, with the reference's
+//    roundings: bf16(g * bf16(x * inv));
+//  * epilogues keep the batch-one GEMV's bf16 boundaries: store, + residual,
+//    SwiGLU over the gate and up strips, or per-row argmax (lowest id on ties).
+#include "common.h"
+
+namespace htn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kStrip = 16;     // output columns per block (MFMA N)
+constexpr int kStep = 32;      // k per MFMA
+constexpr int kMaxRowsMT = 32; // two 16-row tiles
+constexpr int kU = 4;          // k steps in flight per wave
+constexpr int kMaxK = 16384;
+
+struct RowsArgs {
+  const bf16_t* x; long x_rs;
+  const bf16_t* gain; float eps;
+  const bf16_t* w;
+  const bf16_t* res; long res_rs;
+  bf16_t* y; long y_rs;
+  float* part;          // [KS][M][Nw] fp32 (KS > 1)
+  uint64_t* keys;       // argmax: [strips][M]
+  int64_t* tokens;      // argmax: [M]
+  int M, N, K, KS, steps_per_split;
+};
+
+__device__ __forceinline__ float silu_mul_bf(float g, float u) {
+  const float sig = 1.0f / (1.0f + expf(-g));
+  return round_bf(g * sig) * u;
+}
+
+// The 16 bytes of x (row m, k .. k+7) as an A fragment, normalised when the
+// prologue is on. Rows past M and invalid steps give zeros.
+template <bool NORM>
+__device__ __forceinline__ uint4 a_fragment(const RowsArgs& a, int m, int k, bool ok,
+                                            const float* inv) {
+  const int mm = m < a.M ? m : 0;
+  uint4 v = *reinterpret_cast<const uint4*>(a.x + mm * a.x_rs + k);
+  if (NORM) {
+    const uint4 g = *reinterpret_cast<const uint4*>(a.gain + k);
+    float f[8], gf[8];
+    unpack8(v, f);
+    unpack8(g, gf);
+    const float s = inv[mm];
+    v.x = pack_bf2(gf[0] * round_bf(f[0] * s), gf[1] * round_bf(f[1] * s));
+    v.y = pack_bf2(gf[2] * round_bf(f[2] * s), gf[3] * round_bf(f[3] * s));
+    v.z = pack_bf2(gf[4] * round_bf(f[4] * s), gf[5] * round_bf(f[5] * s));
+    v.w = pack_bf2(gf[6] * round_bf(f[6] * s), gf[7] * round_bf(f[7] * s));
+  }
+  const bool live = ok && m < a.M;
+  return live ? v : make_uint4(0, 0, 0, 0);
+}
+
+// Epilogue for one output (row m, column n) given the fp32 dot products of
+// the (gate) column and, for SwiGLU, the up column.
+template <int EPI>
+__device__ __forceinline__ void store_out(const RowsArgs& a, int m, int n, float t0, float t1) {
+  float out;
+  if (EPI == HTN_EPI_STORE) out = t0;
+  else if (EPI == HTN_EPI_RESIDUAL) out = round_bf(t0) + bf2f(a.res[m * a.res_rs + n]);
+  else out = silu_mul_bf(round_bf(t0), round_bf(t1));
+  a.y[m * a.y_rs + n] = static_cast<bf16_t>(f2bf(out));
+}
+
+template <int MT, int S, bool NORM, int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_rows_kernel(RowsArgs a) {
+  __shared__ float inv[kMaxRowsMT];
+  __shared__ float red[4][MT][S][kStrip * 16];
+  __shared__ uint64_t best[kMaxRowsMT][kStrip];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int strip = blockIdx.x, ks = blockIdx.y;
+  const int n0 = strip * kStrip;
+  const int col = lane & 15, quad = lane >> 4;
+  const int Nw = S * a.N;
+  const int j0 = ks * a.steps_per_split;
+  const int total_steps = a.K / kStep;
+  const int j1 = j0 + a.steps_per_split < total_steps ? j0 + a.steps_per_split : total_steps;
+
+  // Weight rows of this lane (clamped to the last row; extra columns are discarded).
+  const bf16_t* wrow[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int n = n0 + col < a.N ? n0 + col : a.N - 1;
+    wrow[s] = a.w + static_cast<long>(n + s * a.N) * a.K + quad * 8;
+  }
+
+  // First batch of weight loads before the norm prologue.
+  uint4 wv[kU][S];
+  auto issue = [&](int jb) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      int j = jb + u * 4;
+      j = j < j1 ? j : j1 - 1;
+#pragma unroll
+      for (int s = 0; s < S; ++s) wv[u][s] = load_stream(wrow[s] + j * kStep);
+    }
+  };
+  issue(j0 + wave);
+
+  if (NORM) {
+    // 1/rms of every row over the full K: wave w reduces rows w, w+4, ...
+    for (int m = wave; m < a.M; m += 4) {
+      float ss = 0.f;
+      for (int k = lane * 8; k < a.K; k += 64 * 8) {
+        float f[8];
+        unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.x_rs + k), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) inv[m] = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+    }
+    __syncthreads();
+  }
+
+  f32x4_t acc[MT][S];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int jb = j0 + wave; jb < j1; jb += 4 * kU) {
+    if (jb != j0 + wave) issue(jb);
+    uint4 av[kU][MT];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int j = jb + u * 4;
+      const bool ok = j < j1;
+      const int k = (ok ? j : j1 - 1) * kStep + quad * 8;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) av[u][t] = a_fragment<NORM>(a, t * 16 + col, k, ok, inv);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+          acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, av[u][t]), __builtin_bit_cast(bf16x8_t, wv[u][s]),
+              acc[t][s], 0, 0, 0);
+  }
+
+  // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + i.
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][s][(quad * 4 + i) * kStrip + col] = acc[t][s][i];
+  __syncthreads();
+
+  // tid -> (row, column) of the strip; MT * 16 rows x 16 columns.
+  for (int o = tid; o < MT * 16 * kStrip; o += kBlock) {
+    const int m = o / kStrip, c = o % kStrip;
+    const int t = m / 16, r = m % 16;
+    float v[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      v[s] = (red[0][t][s][r * kStrip + c] + red[1][t][s][r * kStrip + c]) +
+             (red[2][t][s][r * kStrip + c] + red[3][t][s][r * kStrip + c]);
+    const int n = n0 + c;
+    if (EPI == HTN_EPI_ARGMAX) {
+      if (m < a.M)
+        best[m][c] = n < a.N ? argmax_key(f2bf(v[0]), static_cast<uint32_t>(n)) : 0ull;
+      continue;
+    }
+    if (m >= a.M || n >= a.N) continue;
+    if (a.KS > 1) {
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        a.part[(static_cast<long>(ks) * a.M + m) * Nw + s * a.N + n] = v[s];
+    } else {
+      store_out<EPI>(a, m, n, v[0], S > 1 ? v[S - 1] : 0.f);
+    }
+  }
+  if (EPI == HTN_EPI_ARGMAX) {
+    __syncthreads();
+    if (tid < a.M) {
+      uint64_t b = best[tid][0];
+      for (int c = 1; c < kStrip; ++c) b = best[tid][c] > b ? best[tid][c] : b;
+      a.keys[static_cast<long>(strip) * a.M + tid] = b;
+    }
+  }
+}
+
+// Sum of the K-split partials in split order, then the epilogue.
+template <int S, int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_rows_finish(RowsArgs a) {
+  const long o = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
+  if (o >= static_cast<long>(a.M) * a.N) return;
+  const int m = static_cast<int>(o / a.N), n = static_cast<int>(o % a.N);
+  const int Nw = S * a.N;
+  float v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    float t = 0.f;
+    for (int ks = 0; ks < a.KS; ++ks) t += a.part[(static_cast<long>(ks) * a.M + m) * Nw + s * a.N + n];
+    v[s] = t;
+  }
+  store_out<EPI>(a, m, n, v[0], S > 1 ? v[S - 1] : 0.f);
+}
+
+// Per-row argmax over the strips' keys.
+__global__ __launch_bounds__(kBlock) void gemm_rows_argmax(const uint64_t* __restrict__ keys,
+                                                          int strips, int M, int64_t* tokens) {
+  __shared__ uint64_t wbest[4];
+  const int m = blockIdx.x;
+  uint64_t b = 0;
+  for (int i = threadIdx.x; i < strips; i += kBlock) {
+    const uint64_t k = keys[static_cast<long>(i) * M + m];
+    b = k > b ? k : b;
+  }
+  b = wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t r = wbest[0];
+    for (int i = 1; i < 4; ++i) r = wbest[i] > r ? wbest[i] : r;
+    tokens[m] = static_cast<int64_t>(argmax_key_index(r));
+  }
+}
+
+// K splits: enough blocks for two per CU, whole 4-wave step groups per split.
+int choose_splits(int strips, int K) {
+  const int steps = K / kStep;
+  int ks = (2 * device_cus() + strips - 1) / strips;
+  const int max_ks = steps / 16 > 0 ? steps / 16 : 1;  // at least 16 steps per split
+  if (ks > max_ks) ks = max_ks;
+  if (ks > 8) ks = 8;
+  return ks < 1 ? 1 : ks;
+}
+
+template <int MT, int S, bool NORM, int EPI>
+int launch(RowsArgs& a, hipStream_t st) {
+  const int strips = (a.N + kStrip - 1) / kStrip;
+  hipLaunchKernelGGL((gemm_rows_kernel<MT, S, NORM, EPI>), dim3(strips, a.KS), dim3(kBlock), 0, st, a);
+  if (launch_status() != HTN_OK) return HTN_ELAUNCH;
+  if (EPI == HTN_EPI_ARGMAX) {
+    hipLaunchKernelGGL(gemm_rows_argmax, dim3(a.M), dim3(kBlock), 0, st, a.keys, strips, a.M, a.tokens);
+  } else if (a.KS > 1) {
+    const long outs = static_cast<long>(a.M) * a.N;
+    hipLaunchKernelGGL((gemm_rows_finish<S, EPI>), dim3((outs + kBlock - 1) / kBlock), dim3(kBlock),
+                       0, st, a);
+  }
+  return launch_status();
+}
+
+template <int MT, bool NORM>
+int dispatch_epi(RowsArgs& a, int epi, hipStream_t st) {
+  switch (epi) {
+    case HTN_EPI_STORE: return launch<MT, 1, NORM, HTN_EPI_STORE>(a, st);
+    case HTN_EPI_RESIDUAL: return launch<MT, 1, NORM, HTN_EPI_RESIDUAL>(a, st);
+    case HTN_EPI_SWIGLU: return launch<MT, 2, NORM, HTN_EPI_SWIGLU>(a, st);
+    default: return launch<MT, 1, NORM, HTN_EPI_ARGMAX>(a, st);
+  }
+}
+
+long partial_bytes(long M, long N, long K, int swiglu) {
+  const int strips = static_cast<int>((N + kStrip - 1) / kStrip);
+  const int ks = choose_splits(strips, static_cast<int>(K));
+  return ks > 1 ? static_cast<long>(ks) * M * N * (swiglu ? 2 : 1) * 4 : 0;
+}
+
+}  // namespace
+}  // namespace htn
+
+using namespace htn;
+
+extern "C" int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue) {
+  if (rows <= 0 || rows > kMaxRowsMT || n <= 0 || k <= 0 || k % kStep || k > kMaxK) return 0;
+  if (epilogue == HTN_EPI_ARGMAX) return ((n + kStrip - 1) / kStrip) * rows * 8;
+  return partial_bytes(rows, n, k, epilogue == HTN_EPI_SWIGLU);
+}
+
+extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps,
+                             const void* w, int64_t n, int64_t k, int64_t rows, int epilogue,
+                             const void* residual, int64_t res_stride, void* y, int64_t y_stride,
+                             int64_t* tokens, void* scratch, htn_stream_t stream) {
+  if (!x || !w || rows <= 0 || rows > kMaxRowsMT || n <= 0 || k <= 0 || n > (1L << 31))
+    return HTN_EINVAL;
+  if (epilogue < HTN_EPI_STORE || epilogue > HTN_EPI_ARGMAX) return HTN_EINVAL;
+  if (epilogue == HTN_EPI_ARGMAX ? !tokens || !scratch : !y) return HTN_EINVAL;
+  if (epilogue == HTN_EPI_RESIDUAL && !residual) return HTN_EINVAL;
+  // 16-byte fragments of x, gain and W rows.
+  if (k % kStep || k > kMaxK || x_stride % 8 || !aligned16(x) || !aligned16(w) ||
+      (gain && !aligned16(gain)))
+    return HTN_EUNSUPPORTED;
+  RowsArgs a{};
+  a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
+  a.gain = static_cast<const bf16_t*>(gain); a.eps = eps;
+  a.w = static_cast<const bf16_t*>(w);
+  a.res = static_cast<const bf16_t*>(residual); a.res_rs = res_stride;
+  a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
+  a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
+  const int strips = static_cast<int>((n + kStrip - 1) / kStrip);
+  a.KS = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, a.K);
+  const int steps = a.K / kStep;
+  a.steps_per_split = (steps + a.KS - 1) / a.KS;
+  if (a.KS > 1 && !scratch) return HTN_EINVAL;
+  a.part = static_cast<float*>(scratch);
+  a.keys = static_cast<uint64_t*>(scratch);
+  a.tokens = tokens;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool norm = gain != nullptr;
+  if (rows <= 16)
+    return norm ? dispatch_epi<1, true>(a, epilogue, st) : dispatch_epi<1, false>(a, epilogue, st);
+  return norm ? dispatch_epi<2, true>(a, epilogue, st) : dispatch_epi<2, false>(a, epilogue, st);
+}

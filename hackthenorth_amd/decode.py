@@ -22,6 +22,7 @@ from .kernels.embed import embed_gather
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
+from .kernels.rows import greedy_rows, projection_rows, residual_rows, swiglu_rows
 from .speculate import draft_width, verified_tokens
 
 
@@ -134,8 +135,21 @@ def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=Non
     return out
 
 
+def _attention_chunks(q, keys, values, positions, groups):
+    """grouped_attention over the T queries in chunks the kernel takes at once
+    (at most 8 queries and 32 query rows per kv head)."""
+    t = q.shape[2]
+    step = max(1, min(8, 32 // groups))
+    if t <= step:
+        return grouped_attention(q, keys, values, positions)
+    return torch.cat([grouped_attention(q[:, :, s:s + step], keys, values, positions[s:s + step])
+                      for s in range(0, t, step)], dim=2)
+
+
 def _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings, rotary):
-    """Any batch and token count: per-row GEMVs, batched norm/RoPE/cache and attention."""
+    """Any batch and token count (prefill, verify): multi-row MFMA projections
+    that read each weight once per 32 rows, batched norm/RoPE/cache append and
+    grouped attention. 8-bit weights take the batch-one GEMVs row by row."""
     c = model.config
     b, t = token_ids.shape
     hidden = c.hidden_size
@@ -144,29 +158,43 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
     cos, sin = position_embeddings
     h = embed_gather(token_ids, model.embed_weight).reshape(b * t, hidden)
     widths = c.widths
+    groups = c.num_attention_heads // c.num_key_value_heads
+    rows = b * t
+    multi = not c.quantized
     for i, layer in enumerate(model.layers):
         ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
-        packed = torch.stack([norm_projection(h[r], ln1.weight, layer.qkv_weight,
-                                              ln1.variance_epsilon) for r in range(b * t)])
+        if multi:
+            packed = projection_rows(h, layer.qkv_weight, ln1.weight, ln1.variance_epsilon)
+        else:
+            packed = torch.stack([norm_projection(h[r], ln1.weight, layer.qkv_weight,
+                                                  ln1.variance_epsilon) for r in range(rows)])
         q, k, v = packed.view(b, t, -1).split(widths, -1)
         shape = (b, t, -1, c.head_dim)
         q, _, _ = norm_rope_cache(q.view(shape), k.view(shape), v.view(shape), layer.q_norm,
                                   layer.k_norm, cos, sin, cache.keys[i], cache.values[i],
                                   positions)
-        a = grouped_attention(q, cache.keys[i], cache.values[i], positions)
-        a = a.transpose(1, 2).reshape(b * t, -1).contiguous()
-        r = torch.stack([output_projection_residual(a[j], layer.o_weight, h[j])
-                         for j in range(b * t)])
-        m = torch.stack([norm_projection(r[j], ln2.weight, layer.gate_up_weight,
-                                         ln2.variance_epsilon, swiglu=True)
-                         for j in range(b * t)])
-        h = torch.stack([down_residual(m[j], layer.down_weight, r[j]) for j in range(b * t)])
+        a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
+        a = a.transpose(1, 2).reshape(rows, -1).contiguous()
+        if multi:
+            r = residual_rows(a, layer.o_weight, h)
+            m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
+            h = residual_rows(m, layer.down_weight, r)
+        else:
+            r = torch.stack([output_projection_residual(a[j], layer.o_weight, h[j])
+                             for j in range(rows)])
+            m = torch.stack([norm_projection(r[j], ln2.weight, layer.gate_up_weight,
+                                             ln2.variance_epsilon, swiglu=True)
+                             for j in range(rows)])
+            h = torch.stack([down_residual(m[j], layer.down_weight, r[j]) for j in range(rows)])
     h = h.view(b, t, hidden)
     x = h[:, -1:] if last_only else h
-    rows = x.reshape(-1, hidden).contiguous()
-    out = torch.empty((rows.shape[0],), dtype=torch.int64, device=model.device)
-    for r in range(rows.shape[0]):
-        greedy_head(rows[r], model.norm.weight, model.norm.variance_epsilon,
+    flat = x.reshape(-1, hidden).contiguous()
+    if multi:
+        return greedy_rows(flat, model.lm_head_weight, model.norm.weight,
+                           model.norm.variance_epsilon).view(b, x.shape[1])
+    out = torch.empty((flat.shape[0],), dtype=torch.int64, device=model.device)
+    for r in range(flat.shape[0]):
+        greedy_head(flat[r], model.norm.weight, model.norm.variance_epsilon,
                     model.lm_head_weight, out[r:r + 1])
     return out.view(b, x.shape[1])
 

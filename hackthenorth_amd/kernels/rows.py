@@ -1,0 +1,91 @@
+"""Projections of 2 to 32 rows that read each weight once (MFMA tiles).
+
+The speculative verify pass scores k + 1 tokens in one forward; the reference
+runs its multi-row projections as Triton GEMM tiles (dryft/engine/
+projections.py:168-183, kernels/gateup.py:40-58, kernels/split_down.py:85-101).
+Here every multi-row projection is one htn_gemm_rows launch (plus a K-split
+reduction when the strips alone cannot fill the GPU) with the batch-one
+GEMVs' bf16 rounding boundaries. Larger row counts run in chunks of 32.
+"""
+import torch
+
+from .. import _lib
+
+MAX_ROWS = 32
+
+
+def _scratch(device, rows, n, k, epilogue):
+    nbytes = _lib.load().htn_gemm_rows_scratch_bytes(rows, n, k, epilogue)
+    if nbytes <= 0:
+        return None
+    return torch.empty((nbytes + 7) // 8, dtype=torch.int64, device=device)
+
+
+def _check(x, weight):
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("rows must be a bf16 [M, K] matrix with unit column stride")
+    if weight.dim() != 2 or weight.dtype != torch.bfloat16 or not weight.is_contiguous() \
+            or weight.shape[1] != x.shape[1]:
+        raise ValueError("weight must be a contiguous bf16 [N, K] matrix matching x")
+
+
+def _launch(x, weight, n, epilogue, gain=None, eps=1e-6, residual=None, out=None, tokens=None):
+    rows, k = x.shape
+    scratch = _scratch(x.device, rows, n, k, epilogue)
+    _lib.call("htn_gemm_rows", _lib.ptr(x), x.stride(0), _lib.ptr(gain), float(eps),
+              _lib.ptr(weight), n, k, rows, epilogue, _lib.ptr(residual),
+              residual.stride(0) if residual is not None else 0, _lib.ptr(out),
+              out.stride(0) if out is not None else 0, _lib.ptr(tokens), _lib.ptr(scratch),
+              _lib.stream(x.device))
+
+
+def _chunks(rows):
+    return [(s, min(rows, s + MAX_ROWS)) for s in range(0, rows, MAX_ROWS)]
+
+
+def projection_rows(x, weight, gain=None, eps=1e-6):
+    """bf16(W x_m) for every row m of x [M, K]; gain applies RMSNorm first."""
+    _check(x, weight)
+    _lib.require_gpu(x, weight, gain)
+    out = torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
+    for s, e in _chunks(x.shape[0]):
+        _launch(x[s:e], weight, weight.shape[0], _lib.EPI_STORE, gain, eps, out=out[s:e])
+    return out
+
+
+def residual_rows(x, weight, residual):
+    """bf16(bf16(W x_m) + residual_m) for every row (O and down projections)."""
+    _check(x, weight)
+    if residual.shape != (x.shape[0], weight.shape[0]) or residual.dtype != torch.bfloat16 \
+            or residual.stride(1) != 1:
+        raise ValueError("residual must be bf16 [M, N] with unit column stride")
+    _lib.require_gpu(x, weight, residual)
+    out = torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
+    for s, e in _chunks(x.shape[0]):
+        _launch(x[s:e], weight, weight.shape[0], _lib.EPI_RESIDUAL, residual=residual[s:e],
+                out=out[s:e])
+    return out
+
+
+def swiglu_rows(x, gate_up_weight, gain=None, eps=1e-6):
+    """SwiGLU of the packed gate/up projection ([2I, K]: gate rows, then up rows)."""
+    _check(x, gate_up_weight)
+    if gate_up_weight.shape[0] % 2:
+        raise ValueError("packed gate/up width must be even")
+    _lib.require_gpu(x, gate_up_weight, gain)
+    n = gate_up_weight.shape[0] // 2
+    out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
+    for s, e in _chunks(x.shape[0]):
+        _launch(x[s:e], gate_up_weight, n, _lib.EPI_SWIGLU, gain, eps, out=out[s:e])
+    return out
+
+
+def greedy_rows(x, weight, gain=None, eps=1e-6):
+    """argmax_n bf16(W x_m) per row (lowest id on ties); gain applies RMSNorm first."""
+    _check(x, weight)
+    _lib.require_gpu(x, weight, gain)
+    tokens = torch.empty((x.shape[0],), dtype=torch.int64, device=x.device)
+    for s, e in _chunks(x.shape[0]):
+        _launch(x[s:e], weight, weight.shape[0], _lib.EPI_ARGMAX, gain, eps,
+                tokens=tokens[s:e])
+    return tokens

@@ -41,6 +41,12 @@ extern "C" {
 #define HTN_WEIGHT_INT8 1     /* two's complement int8 */
 #define HTN_WEIGHT_FP8_E4M3 2 /* OCP fp8 e4m3fn (bias 7, no infinities, 0x7f/0xff NaN) */
 
+/* Epilogues of htn_gemm_rows. */
+#define HTN_EPI_STORE 0    /* y = bf16(dot) */
+#define HTN_EPI_RESIDUAL 1 /* y = bf16(bf16(dot) + residual) */
+#define HTN_EPI_SWIGLU 2   /* y = bf16(bf16(silu(bf16 gate)) * bf16 up), w holds 2n rows */
+#define HTN_EPI_ARGMAX 3   /* tokens[m] = argmax_n bf16(dot), lowest id on ties */
+
 typedef void* htn_stream_t;
 
 /* Library version, for the loader's sanity check. */
@@ -156,6 +162,27 @@ int htn_lm_head_argmax_w8(const void* x, const void* gain, float eps, const void
                           const float* scales, int format, int64_t vocab, int64_t k,
                           int64_t* token_out, int64_t* position_inc, void* scratch,
                           htn_stream_t stream);
+
+/* ---------------------------------------------------------------- 2..32 rows
+ * Projection of `rows` (1..32) activation rows x[m, :k] (row stride
+ * x_stride elements) by a row-major bf16 weight w[n, k] (2n rows, gate then
+ * up, for HTN_EPI_SWIGLU), reading the weight once for all rows (MFMA tiles).
+ * gain != NULL applies RMSNorm to each row first:
+ *   x' = bf16(gain * bf16(x * rsqrt(mean(x^2) + eps))).
+ * Epilogues (HTN_EPI_*): y[m, n] (row stride y_stride) as the batch-one GEMVs
+ * round it, + residual[m, n] (row stride res_stride), SwiGLU, or tokens[m]
+ * (int64 device array) = per-row argmax. k must be a multiple of 32, x
+ * (with its stride), gain and w 16-byte aligned.
+ * scratch: htn_gemm_rows_scratch_bytes(rows, n, k, epilogue) bytes (K-split
+ * partials or per-strip argmax keys; 0 means none is needed).
+ * Replaces the reference's multi-row decode projections: Projection._tile
+ * (projections.py:168-183), gate_up_swiglu (kernels/gateup.py:40-58) and the
+ * split down projection (kernels/split_down.py:85-101). */
+int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue);
+int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps, const void* w,
+                  int64_t n, int64_t k, int64_t rows, int epilogue, const void* residual,
+                  int64_t res_stride, void* y, int64_t y_stride, int64_t* tokens, void* scratch,
+                  htn_stream_t stream);
 
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,

@@ -1,0 +1,143 @@
+"""Multi-row (2..32 rows) MFMA projections and the verify forward against the oracle.
+
+Bars: every output within one bf16 ulp of the oracle's rounding of the same
+fp32 dot product (summation order differs; outputs within 1e-4 of zero, where
+cancellation dominates, within 1e-4 absolute) and within max-abs 2e-2 + 2e-2
+relative; argmax ids exact unless the oracle's top-2 gap is below 1e-3;
+the multi-row forward's greedy ids equal the oracle's batched (teacher-forced)
+pass unless the oracle's logit deficit is below 2e-2.
+"""
+import pytest
+import torch
+
+from oracle import qwen3 as Q
+from hackthenorth_amd import decode as D
+from hackthenorth_amd.kernels import gateup as GU
+from hackthenorth_amd.kernels import projection as P
+from hackthenorth_amd.kernels import rows as RW
+from hackthenorth_amd.kernels import split_down as SD
+from hackthenorth_amd.model import Qwen3Model, shape_config
+
+pytestmark = pytest.mark.gpu
+
+
+def nrm(stream, shape, std=1.0, seed=11):
+    return Q.normal_bf16(seed, stream, shape, std)
+
+
+def within_one_ulp(actual, expected):
+    a = actual.detach().cpu().float().reshape(-1)
+    e = expected.float().reshape(-1)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(e.abs().clamp_min(1e-30))) - 7)
+    bad = (a - e).abs() > torch.maximum(ulp, torch.full_like(ulp, 1e-4))
+    assert not bool(bad.any()), (int(bad.sum()), a[bad][:4], e[bad][:4])
+    torch.testing.assert_close(a, e, atol=2e-2, rtol=2e-2)
+
+
+SHAPES = [(4096, 1024), (257, 2560), (40, 4096), (100, 12288), (1536, 9728), (3, 32)]
+ROWS = [2, 5, 8, 16, 17, 32]
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", ROWS)
+def test_projection_rows_match_oracle(m, n, k):
+    w = nrm(30, (2 * n, k), std=0.02)
+    x, g, res = nrm(31, (m, k)), nrm(32, (k,)), nrm(33, (m, n))
+    wd, xd, gd, rd = w.cuda(), x.cuda(), g.cuda(), res.cuda()
+    top = wd[:n].contiguous()
+    within_one_ulp(RW.projection_rows(xd, top), Q.linear(x, w[:n]))
+    normed = Q.rms_norm(x, g, 1e-6)
+    within_one_ulp(RW.projection_rows(xd, top, gd, 1e-6), Q.linear(normed, w[:n]))
+    expected = Q.output_residual(x, w[:n], res)
+    torch.testing.assert_close(RW.residual_rows(xd, top, rd).cpu().float(), expected.float(),
+                               atol=2e-2, rtol=2e-2)
+    gu = Q.linear(normed, w)
+    torch.testing.assert_close(RW.swiglu_rows(xd, wd, gd, 1e-6).cpu().float(),
+                               Q.silu_mul(gu[:, :n], gu[:, n:]).float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8, 32])
+def test_rows_match_the_batch_one_gemvs(m):
+    n, k = 1024, 3072
+    w = nrm(34, (2 * n, k), std=0.02).cuda()
+    x, g = nrm(35, (m, k)).cuda(), nrm(36, (k,)).cuda()
+    rows = RW.projection_rows(x, w[:n].contiguous(), g, 1e-6)
+    for r in range(m):
+        one = P.norm_projection(x[r:r + 1].contiguous(), g, w[:n].contiguous(), 1e-6)
+        within_one_ulp(rows[r], one.cpu().reshape(-1))
+
+
+@pytest.mark.parametrize("m", [2, 5, 32])
+def test_greedy_rows_match_oracle_argmax(m):
+    v, k = 151936, 1024
+    w = nrm(37, (v, k), std=0.02)
+    x, g = nrm(38, (m, k), std=2.0), nrm(39, (k,))
+    tokens = RW.greedy_rows(x.cuda(), w.cuda(), g.cuda(), 1e-6).cpu()
+    logits = Q.rms_norm(x, g, 1e-6).float() @ w.float().T
+    for r in range(m):
+        expected = int(Q.greedy(logits[r].to(torch.bfloat16)))
+        got = int(tokens[r])
+        if got != expected:
+            assert float(logits[r, expected] - logits[r, got]) < 1e-3, (r, got, expected)
+
+
+def test_greedy_rows_ties_choose_lowest_id():
+    v, k = 151936, 1024
+    w = torch.zeros(v, k, dtype=torch.bfloat16, device="cuda")
+    w[3].fill_(1)
+    w[-1].fill_(1)
+    x = torch.ones(4, k, dtype=torch.bfloat16, device="cuda")
+    assert RW.greedy_rows(x, w).tolist() == [3, 3, 3, 3]
+
+
+def test_gate_up_swiglu_interleaved_layout():
+    m, k, inter = 5, 2560, 9728
+    gate, up = nrm(40, (inter, k), std=0.02), nrm(41, (inter, k), std=0.02)
+    interleaved = torch.stack((gate.t(), up.t()), dim=-1).reshape(k, 2 * inter)
+    x = nrm(42, (1, m, k))
+    out = GU.gate_up_swiglu(x.cuda(), interleaved.cuda())
+    assert out.shape == (1, m, inter)
+    expected = Q.silu_mul(Q.linear(x, gate), Q.linear(x, up))
+    torch.testing.assert_close(out.cpu().float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+def test_split_down_residual_norm():
+    m, k, n = 4, 9728, 2560
+    w = nrm(43, (n, k), std=0.02)
+    x, res, g = nrm(44, (m, k)), nrm(45, (m, n)), nrm(46, (n,))
+    out, normed = SD.split_down_residual_norm(x.cuda(), w.cuda(), res.cuda(), g.cuda(), 1e-6)
+    expected = Q.output_residual(x, w, res)
+    torch.testing.assert_close(out.cpu().float(), expected.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(normed.cpu().float(), Q.rms_norm(out.cpu(), g, 1e-6).float(),
+                               atol=2e-2, rtol=2e-2)
+    # The strided (transposed-storage) weight the reference accepts.
+    out2 = SD.split_down_residual(x.cuda(), w.t().contiguous().t().cuda(), res.cuda())
+    torch.testing.assert_close(out2.cpu().float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("length", [2, 5, 8])
+def test_multi_row_forward_matches_oracle(length):
+    cfg = shape_config("tiny", seed=0)
+    model = Qwen3Model.random(cfg, seed=0)
+    shape = Q.SHAPES["tiny"]
+    prompt = Q.prompt_ids(9, 97, seed=1)
+    capacity = len(prompt) + length + 4
+    oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), capacity)
+    proposal = Q.prompt_ids(length, 97, seed=4)
+    seq = prompt + proposal
+    _, logits, _ = oracle.forward(torch.tensor([seq]), Q.new_cache(shape, capacity),
+                                  torch.arange(len(seq)), last_only=False)
+    with torch.inference_mode():
+        cache = D.KVCache(model, 1, capacity)
+        rotary = D.RotaryTable(model, capacity)
+        # Prompt rows (all but the last) in one multi-row pass, then the verify rows.
+        D.forward(model, torch.tensor([prompt[:-1]], device="cuda"), cache,
+                  torch.arange(len(prompt) - 1, device="cuda"), rotary=rotary)
+        rows = torch.tensor([[prompt[-1]] + proposal], device="cuda")
+        pos = torch.arange(len(prompt) - 1, len(seq), device="cuda")
+        got = D.forward(model, rows, cache, pos, last_only=False, rotary=rotary)[0].cpu()
+    lf = logits[0, len(prompt) - 1:]
+    for i, tok in enumerate(got.tolist()):
+        o = int(lf[i].to(torch.bfloat16).float().argmax())
+        if tok != o:
+            assert float(lf[i].max() - lf[i][tok]) < 2e-2, (i, tok, o)
