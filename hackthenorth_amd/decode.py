@@ -247,6 +247,8 @@ class DecodeState:
         self.verify_graph = None
         if output_length > 1:
             self.capture(model)
+        if self.draft_tokens > 0:
+            self.capture_verifier(model)
 
     def step(self, model):
         forward(model, self.token, self.cache, self.position, rotary=self.rotary,
@@ -294,14 +296,48 @@ class DecodeState:
             self.position.fill_(length)
         return self.token
 
+    def verify_step(self, model):
+        """Forward of the verify input at positions position .. position + k
+        (decode.py:168-179): every row's greedy token, multi-row projections."""
+        positions = self.position + self.verify_offsets
+        return forward(model, self.verify_input, self.cache, positions, last_only=False,
+                       rotary=self.rotary)
+
+    def capture_verifier(self, model):
+        """Capture verify_step as a graph over a fixed-address input (decode.py:181-195)."""
+        length = self.draft_tokens + 1
+        device = model.device
+        self.verify_input = torch.zeros((1, length), dtype=torch.int64, device=device)
+        self.verify_offsets = torch.arange(length, device=device)
+        prompt_length = self.shape[1]
+        self.position.fill_(prompt_length)
+        stream = torch.cuda.Stream(device=device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                self.verify_step(model)
+        torch.cuda.current_stream(device).wait_stream(stream)
+        self.verify_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.verify_graph, stream=stream):
+            self.verify_output = self.verify_step(model)
+        self.position.fill_(prompt_length)
+
     def verify(self, current_token, proposal, position):
         """Score [current, *proposal] at positions position.. in one pass and keep
-        the verified prefix plus one target token (decode.py:197-206)."""
+        the verified prefix plus one target token (decode.py:197-206). A
+        proposal of the captured width replays the verify graph."""
         inputs = torch.tensor([[current_token, *proposal]], dtype=torch.int64,
                               device=self.token.device)
-        positions = torch.arange(position, position + inputs.shape[1], device=self.token.device)
-        predictions = forward(self.model, inputs, self.cache, positions, last_only=False,
-                              rotary=self.rotary)
+        if self.verify_graph is not None and inputs.shape[1] == self.verify_input.shape[1]:
+            self.verify_input.copy_(inputs)
+            self.position.fill_(position)
+            self.verify_graph.replay()
+            predictions = self.verify_output
+        else:
+            positions = torch.arange(position, position + inputs.shape[1],
+                                     device=self.token.device)
+            predictions = forward(self.model, inputs, self.cache, positions, last_only=False,
+                                  rotary=self.rotary)
         emitted = verified_tokens(proposal, predictions[0].tolist())
         self.token.copy_(predictions[:, len(emitted) - 1:len(emitted)])
         # The speculative tail is discarded logically: later queries mask it and
