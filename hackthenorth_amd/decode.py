@@ -86,7 +86,9 @@ class RotaryTable:
         return row[:, :HEAD_DIM], row[:, HEAD_DIM:]
 
     def select(self, positions):
-        return tuple(t.index_select(1, positions) for t in self.tables)
+        """(cos, sin) rows [1, T, 128] for device positions; a position outside
+        the table gives zero rows (the gather kernel checks every id)."""
+        return tuple(embed_gather(positions.reshape(-1), t[0]).unsqueeze(0) for t in self.tables)
 
 
 def decode_layer(model, i, h, cache, position, rotary, rope=None):
@@ -229,12 +231,18 @@ class DecodeState:
     """Cache, rotary table, device token/position and the captured step (decode.py:102-206)."""
 
     def __init__(self, model, batch_size, prompt_length, output_length, speculative=False,
-                 cache_rotary=True, omit_unused_masks=True):
+                 cache_rotary=True, omit_unused_masks=True, draft_tokens=None):
         self.shape = (batch_size, prompt_length, output_length)
         self.draft_tokens = draft_width(output_length) if speculative and batch_size == 1 else 0
+        if speculative and batch_size == 1 and draft_tokens is not None:
+            self.draft_tokens = int(draft_tokens)  # a draft model's fixed proposal width
         # Tail verification may write beyond the last requested output; causal
         # attention hides those scratch slots from earlier queries.
         capacity = prompt_length + output_length - 1 + self.draft_tokens
+        if self.draft_tokens:
+            # The verifier is captured at the prompt length: its k + 1 rows
+            # need slots there even for a one-token request.
+            capacity = max(capacity, prompt_length + self.draft_tokens + 1)
         device = model.device
         self.model = model
         self.capacity = capacity

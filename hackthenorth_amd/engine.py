@@ -7,25 +7,41 @@ max_new_tokens times, greedy, never stopping at end-of-sequence ids.
 import torch
 
 from .decode import DecodeState, stream_decode
+from .draft import DraftSpeculator
 from .model import Qwen3Model
 from .speculate import BackoffPromptLookup
 
 
 class Engine:
-    def __init__(self, model_path: str, speculative: bool = True, device="cuda") -> None:
+    def __init__(self, model_path: str, speculative: bool = True, device="cuda",
+                 draft_model_path: str = None, draft_tokens: int = 4) -> None:
         """Load config.json (+ safetensors, or the seeded random init) onto the GPU.
 
         speculative=False disables the batch-one prompt-lookup verifier, giving
-        one decode step per output token.
+        one decode step per output token. draft_model_path (same vocabulary)
+        switches batch-one speculation from prompt lookup to a draft model
+        proposing draft_tokens tokens per target verify pass.
         """
         if not torch.cuda.is_available():
             raise RuntimeError("Engine needs a HIP GPU")
         self.model = Qwen3Model.from_pretrained(model_path, device)
+        self.draft = (Qwen3Model.from_pretrained(draft_model_path, device)
+                      if draft_model_path else None)
+        self.draft_tokens = draft_tokens
         self.speculative = speculative
         self.state = None
+        self.speculator = None
 
     def generate(self, input_ids: list, max_new_tokens: int):
         if max_new_tokens <= 0:
+            return
+        if self.draft is not None and self.speculative and len(input_ids) == 1:
+            shape = (1, len(input_ids[0]), max_new_tokens)
+            if self.speculator is None or self.speculator.shape != shape:
+                self.speculator = None
+                self.speculator = DraftSpeculator(self.model, self.draft, shape[1], shape[2],
+                                                  self.draft_tokens)
+            yield from self.speculator.generate(input_ids[0], max_new_tokens)
             return
         with torch.inference_mode():
             shape = (len(input_ids), len(input_ids[0]), max_new_tokens)
