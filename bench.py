@@ -23,7 +23,12 @@ Also reported on the same line:
                 the Qwen3-8B shape with weight-only int8 / fp8-e4m3fn projections
                 and LM head (uniform integer weights in [-127, 127], per-row
                 scales U(0.001, 0.01)), decoding 128 steps at context 8192 over a
-                synthetic KV cache (N(0,1) keys and values in slots 0..8191).
+                synthetic KV cache (N(0,1) keys and values in slots 0..8191);
+  speculative_4b_draft_0.6b
+                Qwen3-4B-shape target with a Qwen3-0.6B-shape draft (both random
+                bf16), k = 4 draft tokens verified in one 5-row pass, context 4096
+                (synthetic KV caches): tok/s, measured greedy acceptance, and the
+                verify pass / draft step / single target step times.
 """
 import argparse
 import json
@@ -118,6 +123,65 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
                 tokens=tokens.cpu().tolist(), elapsed=elapsed, tok_s=tok_s,
                 ms_per_step=1e3 * elapsed / steps, bytes_per_token=bytes_per_token,
                 decode_frac=bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9))
+
+
+def graph_ms(graph, reps=20):
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def run_draft_speculation(ctx, steps, k, log):
+    """4B target + 0.6B draft at context `ctx` over synthetic KV caches."""
+    from hackthenorth_amd.draft import DraftSpeculator
+    target = Qwen3Model.random(shape_config("qwen3-4b"))
+    draft = Qwen3Model.random(shape_config("qwen3-0.6b"))
+    spec = DraftSpeculator(target, draft, ctx, steps + 1, draft_tokens=k)
+    prompt = DR.randint(ctx, target.config.vocab_size, PROMPT_SEED, PROMPT_STREAM)
+    first = int(prompt[-1])
+    with torch.inference_mode():
+        for st in (spec.target_state, spec.draft_state):
+            DR.normal_(st.cache.storage.view(-1), 21, 78, 1.0)
+        ts, ds = spec.target_state, spec.draft_state
+        # Component times at this context.
+        ts.position.fill_(ctx)
+        verify_ms = graph_ms(ts.verify_graph)
+        ts.position.fill_(ctx)
+        step_ms = graph_ms(ts.graph)
+        ds.position.fill_(ctx)
+        draft_ms = graph_ms(spec.draft_graph)
+        list(spec.continue_from(first, ctx, 8))  # warm-up
+        spec.reset_stats()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tokens = [t[0] for t in spec.continue_from(first, ctx, steps)]
+        elapsed = time.perf_counter() - t0
+    alpha = spec.acceptance
+    cycle_ms = 1e3 * elapsed / max(spec.cycles, 1)
+
+    def projected(a):  # tokens per cycle at per-token acceptance a, measured cycle time
+        per_cycle = (1 - a ** (k + 1)) / (1 - a) if a < 1 else k + 1
+        return round(per_cycle / (cycle_ms / 1e3), 1)
+
+    log(f"speculation 4b+0.6b k={k}: {steps / elapsed:.1f} tok/s, acceptance {alpha:.3f}, "
+        f"verify {verify_ms:.3f} ms, target step {step_ms:.3f} ms, draft k steps {draft_ms:.3f} ms")
+    return {"workload": f"Qwen3-4B-shape target + Qwen3-0.6B-shape draft (random bf16), k={k} "
+                        f"draft tokens, {k + 1}-row verify pass, context {ctx} (synthetic KV), "
+                        f"{steps} tokens",
+            "tok_s": round(steps / elapsed, 2), "acceptance": round(alpha, 4),
+            "cycles": spec.cycles, "tokens_per_cycle": round(steps / max(spec.cycles, 1), 3),
+            "cycle_ms": round(cycle_ms, 4), "verify_pass_ms": round(verify_ms, 4),
+            "target_step_ms": round(step_ms, 4), "draft_k_steps_ms": round(draft_ms, 4),
+            "verify_over_step": round(verify_ms / step_ms, 3),
+            "target_only_tok_s": round(1e3 / step_ms, 1),
+            "projected_tok_s_at_acceptance": {str(a): projected(a) for a in (0.5, 0.7, 0.9)},
+            "first_tokens": tokens[:8]}
 
 
 def dominant_kernel(model, launches=280):
@@ -370,6 +434,12 @@ def main():
                     f"({100 * rq['decode_frac']:.1f}% of roofline)")
             except Exception as exc:
                 line[key] = {"error": repr(exc)}
+    if not args.no_8b:
+        try:
+            line["speculative_4b_draft_0.6b"] = run_draft_speculation(4096, 128, 4, log)
+        except Exception as exc:
+            line["speculative_4b_draft_0.6b"] = {"error": repr(exc)}
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["prompt"], res["tokens"], res["first"])
     print(json.dumps(line), flush=True)

@@ -46,7 +46,7 @@ SIGNATURES = {
     "htn_gemv_norm_w8": [_P, _P, _F, _P, _P, _I, _P, _I64, _I64, _I, _P],
     "htn_gemv_residual_w8": [_P, _P, _P, _I, _P, _P, _I64, _I64, _P],
     "htn_lm_head_argmax_w8": [_P, _P, _F, _P, _P, _I, _I64, _I64, _P, _P, _P, _P],
-    "htn_gemm_rows_scratch_bytes": [_I64, _I64, _I64, _I],
+    "htn_gemm_rows_scratch_bytes": [_I64, _I64, _I64, _I, _I],
     "htn_gemm_rows": [_P, _I64, _P, _F, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P,
                       _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],

@@ -5,16 +5,20 @@
 // v_mfma_f32_16x16x32_bf16 (one or two 16-row tiles, rows past M are zero),
 // a strip of 16 weight rows the B operand. The kernel stays HBM-bound on W:
 //
-//  * block = 4 waves on one 16-column strip (plus the matching up strip for
-//    SwiGLU); the waves take interleaved 32-wide k steps of the block's K
-//    range, each lane loading 16 contiguous bytes of one weight row per step,
-//    U steps in flight;
-//  * when the strips alone cannot fill the GPU, K is split over KS blocks
-//    whose fp32 partials a second, stream-ordered launch sums in a fixed
-//    order (deterministic) before the epilogue;
-//  * the optional RMSNorm prologue computes each row's 1/rms once per block
-//    and normalises x fragments as they are loaded, with the reference's
-//    roundings: bf16(g * bf16(x * inv));
+//  * block = W waves (4 to 16, more when strips are few) on one 16-column
+//    strip (plus the matching up strip for SwiGLU); the waves take
+//    interleaved 64-wide k steps, each lane loading 32 contiguous bytes of one
+//    weight row per step (a 16-row x 128-byte tile per step, whole cache
+//    lines per wave), U steps in flight, and reduce through LDS, so every
+//    output is finished by the block that computed it. Within a step the two
+//    MFMAs see k permuted identically in A and B (lane quad q holds k offsets
+//    16q .. 16q+15), which leaves each dot product unchanged;
+//  * only when even 16 waves per strip cannot fill the GPU is K split over
+//    KS blocks, whose fp32 partials a second, stream-ordered launch sums in a
+//    fixed order (deterministic) before the epilogue;
+//  * the optional RMSNorm runs once, as a row-norm launch into the scratch
+//    buffer (reference roundings bf16(g * bf16(x * inv))), instead of in every
+//    block;
 //  * epilogues keep the batch-one GEMV's bf16 boundaries: store, + residual,
 //    SwiGLU over the gate and up strips, or per-row argmax (lowest id on ties).
 #include "common.h"
@@ -26,14 +30,14 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kStrip = 16;     // output columns per block (MFMA N)
-constexpr int kStep = 32;      // k per MFMA
+constexpr int kStep = 64;      // k per step: two MFMAs of 32
 constexpr int kMaxRowsMT = 32; // two 16-row tiles
-constexpr int kU = 4;          // k steps in flight per wave
+constexpr int kU = 2;          // k steps (32 bytes per lane per weight row) in flight per wave
+constexpr int kMaxWaves = 16;
 constexpr int kMaxK = 16384;
 
 struct RowsArgs {
   const bf16_t* x; long x_rs;
-  const bf16_t* gain; float eps;
   const bf16_t* w;
   const bf16_t* res; long res_rs;
   bf16_t* y; long y_rs;
@@ -43,31 +47,20 @@ struct RowsArgs {
   int M, N, K, KS, steps_per_split;
 };
 
+constexpr long kAlign = 256;
+long align_up(long v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
 __device__ __forceinline__ float silu_mul_bf(float g, float u) {
   const float sig = 1.0f / (1.0f + expf(-g));
   return round_bf(g * sig) * u;
 }
 
-// The 16 bytes of x (row m, k .. k+7) as an A fragment, normalised when the
-// prologue is on. Rows past M and invalid steps give zeros.
-template <bool NORM>
-__device__ __forceinline__ uint4 a_fragment(const RowsArgs& a, int m, int k, bool ok,
-                                            const float* inv) {
+// The 16 bytes of x (row m, k .. k+7) as an A fragment; rows past M and
+// invalid steps give zeros.
+__device__ __forceinline__ uint4 a_fragment(const RowsArgs& a, int m, int k, bool ok) {
   const int mm = m < a.M ? m : 0;
-  uint4 v = *reinterpret_cast<const uint4*>(a.x + mm * a.x_rs + k);
-  if (NORM) {
-    const uint4 g = *reinterpret_cast<const uint4*>(a.gain + k);
-    float f[8], gf[8];
-    unpack8(v, f);
-    unpack8(g, gf);
-    const float s = inv[mm];
-    v.x = pack_bf2(gf[0] * round_bf(f[0] * s), gf[1] * round_bf(f[1] * s));
-    v.y = pack_bf2(gf[2] * round_bf(f[2] * s), gf[3] * round_bf(f[3] * s));
-    v.z = pack_bf2(gf[4] * round_bf(f[4] * s), gf[5] * round_bf(f[5] * s));
-    v.w = pack_bf2(gf[6] * round_bf(f[6] * s), gf[7] * round_bf(f[7] * s));
-  }
-  const bool live = ok && m < a.M;
-  return live ? v : make_uint4(0, 0, 0, 0);
+  const uint4 v = *reinterpret_cast<const uint4*>(a.x + mm * a.x_rs + k);
+  return ok && m < a.M ? v : make_uint4(0, 0, 0, 0);
 }
 
 // Epilogue for one output (row m, column n) given the fp32 dot products of
@@ -81,10 +74,9 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, int m, int n, float
   a.y[m * a.y_rs + n] = static_cast<bf16_t>(f2bf(out));
 }
 
-template <int MT, int S, bool NORM, int EPI>
-__global__ __launch_bounds__(kBlock) void gemm_rows_kernel(RowsArgs a) {
-  __shared__ float inv[kMaxRowsMT];
-  __shared__ float red[4][MT][S][kStrip * 16];
+template <int MT, int S, int EPI, int W>
+__global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
+  __shared__ float red[W][MT][S][kStrip * 16];
   __shared__ uint64_t best[kMaxRowsMT][kStrip];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int strip = blockIdx.x, ks = blockIdx.y;
@@ -100,37 +92,23 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_kernel(RowsArgs a) {
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const int n = n0 + col < a.N ? n0 + col : a.N - 1;
-    wrow[s] = a.w + static_cast<long>(n + s * a.N) * a.K + quad * 8;
+    wrow[s] = a.w + static_cast<long>(n + s * a.N) * a.K + quad * 16;
   }
 
-  // First batch of weight loads before the norm prologue.
-  uint4 wv[kU][S];
+  uint4 wv[kU][S][2];
   auto issue = [&](int jb) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      int j = jb + u * 4;
+      int j = jb + u * W;
       j = j < j1 ? j : j1 - 1;
 #pragma unroll
-      for (int s = 0; s < S; ++s) wv[u][s] = load_stream(wrow[s] + j * kStep);
+      for (int s = 0; s < S; ++s) {
+        wv[u][s][0] = *reinterpret_cast<const uint4*>(wrow[s] + j * kStep);
+        wv[u][s][1] = *reinterpret_cast<const uint4*>(wrow[s] + j * kStep + 8);
+      }
     }
   };
   issue(j0 + wave);
-
-  if (NORM) {
-    // 1/rms of every row over the full K: wave w reduces rows w, w+4, ...
-    for (int m = wave; m < a.M; m += 4) {
-      float ss = 0.f;
-      for (int k = lane * 8; k < a.K; k += 64 * 8) {
-        float f[8];
-        unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.x_rs + k), f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) inv[m] = 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
-    }
-    __syncthreads();
-  }
 
   f32x4_t acc[MT][S];
 #pragma unroll
@@ -138,26 +116,31 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int s = 0; s < S; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int jb = j0 + wave; jb < j1; jb += 4 * kU) {
+  for (int jb = j0 + wave; jb < j1; jb += W * kU) {
     if (jb != j0 + wave) issue(jb);
-    uint4 av[kU][MT];
+    uint4 av[kU][MT][2];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int j = jb + u * 4;
+      const int j = jb + u * W;
       const bool ok = j < j1;
-      const int k = (ok ? j : j1 - 1) * kStep + quad * 8;
+      const int k = (ok ? j : j1 - 1) * kStep + quad * 16;
 #pragma unroll
-      for (int t = 0; t < MT; ++t) av[u][t] = a_fragment<NORM>(a, t * 16 + col, k, ok, inv);
+      for (int t = 0; t < MT; ++t) {
+        av[u][t][0] = a_fragment(a, t * 16 + col, k, ok);
+        av[u][t][1] = a_fragment(a, t * 16 + col, k + 8, ok);
+      }
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u)
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-          acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, av[u][t]), __builtin_bit_cast(bf16x8_t, wv[u][s]),
-              acc[t][s], 0, 0, 0);
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, av[u][t][h]),
+                __builtin_bit_cast(bf16x8_t, wv[u][s][h]), acc[t][s], 0, 0, 0);
   }
 
   // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + i.
@@ -170,14 +153,17 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_kernel(RowsArgs a) {
   __syncthreads();
 
   // tid -> (row, column) of the strip; MT * 16 rows x 16 columns.
-  for (int o = tid; o < MT * 16 * kStrip; o += kBlock) {
+  for (int o = tid; o < MT * 16 * kStrip; o += W * 64) {
     const int m = o / kStrip, c = o % kStrip;
     const int t = m / 16, r = m % 16;
     float v[S];
 #pragma unroll
-    for (int s = 0; s < S; ++s)
-      v[s] = (red[0][t][s][r * kStrip + c] + red[1][t][s][r * kStrip + c]) +
-             (red[2][t][s][r * kStrip + c] + red[3][t][s][r * kStrip + c]);
+    for (int s = 0; s < S; ++s) {
+      float sum = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) sum += red[ww][t][s][r * kStrip + c];
+      v[s] = sum;
+    }
     const int n = n0 + c;
     if (EPI == HTN_EPI_ARGMAX) {
       if (m < a.M)
@@ -240,20 +226,31 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_argmax(const uint64_t* __res
   }
 }
 
-// K splits: enough blocks for two per CU, whole 4-wave step groups per split.
-int choose_splits(int strips, int K) {
+// Waves per strip: enough for about 16 waves per CU, 4 to 16 per block, and
+// at least two k steps per wave. K splits across blocks only when 16 waves
+// per strip still leave the GPU under-filled.
+int choose_waves(int strips, int K) {
+  const long target = 16L * device_cus();
+  int w = 4;
+  while (w < kMaxWaves && static_cast<long>(strips) * w < target && (K / kStep) >= 4 * w) w *= 2;
+  return w;
+}
+
+int choose_splits(int strips, int waves, int K) {
   const int steps = K / kStep;
-  int ks = (2 * device_cus() + strips - 1) / strips;
-  const int max_ks = steps / 16 > 0 ? steps / 16 : 1;  // at least 16 steps per split
+  const long target = 16L * device_cus();
+  int ks = static_cast<int>((target + static_cast<long>(strips) * waves - 1) /
+                            (static_cast<long>(strips) * waves));
+  const int max_ks = steps / (4 * waves) > 0 ? steps / (4 * waves) : 1;  // 4 steps per wave
   if (ks > max_ks) ks = max_ks;
   if (ks > 8) ks = 8;
   return ks < 1 ? 1 : ks;
 }
 
-template <int MT, int S, bool NORM, int EPI>
-int launch(RowsArgs& a, hipStream_t st) {
+template <int MT, int S, int EPI, int W>
+int launch_w(RowsArgs& a, hipStream_t st) {
   const int strips = (a.N + kStrip - 1) / kStrip;
-  hipLaunchKernelGGL((gemm_rows_kernel<MT, S, NORM, EPI>), dim3(strips, a.KS), dim3(kBlock), 0, st, a);
+  hipLaunchKernelGGL((gemm_rows_kernel<MT, S, EPI, W>), dim3(strips, a.KS), dim3(W * 64), 0, st, a);
   if (launch_status() != HTN_OK) return HTN_ELAUNCH;
   if (EPI == HTN_EPI_ARGMAX) {
     hipLaunchKernelGGL(gemm_rows_argmax, dim3(a.M), dim3(kBlock), 0, st, a.keys, strips, a.M, a.tokens);
@@ -265,20 +262,37 @@ int launch(RowsArgs& a, hipStream_t st) {
   return launch_status();
 }
 
-template <int MT, bool NORM>
-int dispatch_epi(RowsArgs& a, int epi, hipStream_t st) {
+template <int MT, int S, int EPI>
+int launch(RowsArgs& a, int waves, hipStream_t st) {
+  if (waves >= 16) return launch_w<MT, S, EPI, 16>(a, st);
+  if (waves >= 8) return launch_w<MT, S, EPI, 8>(a, st);
+  return launch_w<MT, S, EPI, 4>(a, st);
+}
+
+template <int MT>
+int dispatch_epi(RowsArgs& a, int epi, int waves, hipStream_t st) {
   switch (epi) {
-    case HTN_EPI_STORE: return launch<MT, 1, NORM, HTN_EPI_STORE>(a, st);
-    case HTN_EPI_RESIDUAL: return launch<MT, 1, NORM, HTN_EPI_RESIDUAL>(a, st);
-    case HTN_EPI_SWIGLU: return launch<MT, 2, NORM, HTN_EPI_SWIGLU>(a, st);
-    default: return launch<MT, 1, NORM, HTN_EPI_ARGMAX>(a, st);
+    case HTN_EPI_STORE: return launch<MT, 1, HTN_EPI_STORE>(a, waves, st);
+    case HTN_EPI_RESIDUAL: return launch<MT, 1, HTN_EPI_RESIDUAL>(a, waves, st);
+    case HTN_EPI_SWIGLU: return launch<MT, 2, HTN_EPI_SWIGLU>(a, waves, st);
+    default: return launch<MT, 1, HTN_EPI_ARGMAX>(a, waves, st);
   }
 }
 
-long partial_bytes(long M, long N, long K, int swiglu) {
+struct Plan {
+  int waves, ks;
+  long norm_bytes, tail_bytes;
+};
+
+Plan plan(long M, long N, long K, int epilogue, bool norm) {
+  Plan p{};
   const int strips = static_cast<int>((N + kStrip - 1) / kStrip);
-  const int ks = choose_splits(strips, static_cast<int>(K));
-  return ks > 1 ? static_cast<long>(ks) * M * N * (swiglu ? 2 : 1) * 4 : 0;
+  p.waves = choose_waves(strips, static_cast<int>(K));
+  p.ks = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, p.waves, static_cast<int>(K));
+  p.norm_bytes = norm ? align_up(M * K * 2) : 0;
+  if (epilogue == HTN_EPI_ARGMAX) p.tail_bytes = static_cast<long>(strips) * M * 8;
+  else if (p.ks > 1) p.tail_bytes = static_cast<long>(p.ks) * M * N * (epilogue == HTN_EPI_SWIGLU ? 2 : 1) * 4;
+  return p;
 }
 
 }  // namespace
@@ -286,11 +300,15 @@ long partial_bytes(long M, long N, long K, int swiglu) {
 
 using namespace htn;
 
-extern "C" int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue) {
+extern "C" int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue,
+                                               int norm) {
   if (rows <= 0 || rows > kMaxRowsMT || n <= 0 || k <= 0 || k % kStep || k > kMaxK) return 0;
-  if (epilogue == HTN_EPI_ARGMAX) return ((n + kStrip - 1) / kStrip) * rows * 8;
-  return partial_bytes(rows, n, k, epilogue == HTN_EPI_SWIGLU);
+  const Plan p = plan(rows, n, k, epilogue, norm != 0);
+  return p.norm_bytes + p.tail_bytes;
 }
+
+extern "C" int htn_rms_norm(const void* x, int64_t x_row_stride, const void* gain, void* out,
+                            int64_t rows, int64_t cols, float eps, htn_stream_t stream);
 
 extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps,
                              const void* w, int64_t n, int64_t k, int64_t rows, int epilogue,
@@ -299,30 +317,36 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   if (!x || !w || rows <= 0 || rows > kMaxRowsMT || n <= 0 || k <= 0 || n > (1L << 31))
     return HTN_EINVAL;
   if (epilogue < HTN_EPI_STORE || epilogue > HTN_EPI_ARGMAX) return HTN_EINVAL;
-  if (epilogue == HTN_EPI_ARGMAX ? !tokens || !scratch : !y) return HTN_EINVAL;
+  if (epilogue == HTN_EPI_ARGMAX ? !tokens : !y) return HTN_EINVAL;
   if (epilogue == HTN_EPI_RESIDUAL && !residual) return HTN_EINVAL;
   // 16-byte fragments of x, gain and W rows.
   if (k % kStep || k > kMaxK || x_stride % 8 || !aligned16(x) || !aligned16(w) ||
       (gain && !aligned16(gain)))
     return HTN_EUNSUPPORTED;
+  const Plan p = plan(rows, n, k, epilogue, gain != nullptr);
+  if ((p.norm_bytes + p.tail_bytes) > 0 && !scratch) return HTN_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
   RowsArgs a{};
   a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
-  a.gain = static_cast<const bf16_t*>(gain); a.eps = eps;
+  if (gain) {
+    // Rows normalised once into the scratch buffer.
+    bf16_t* xn = static_cast<bf16_t*>(scratch);
+    const int rc = htn_rms_norm(x, x_stride, gain, xn, rows, k, eps, stream);
+    if (rc != HTN_OK) return rc;
+    a.x = xn;
+    a.x_rs = k;
+  }
   a.w = static_cast<const bf16_t*>(w);
   a.res = static_cast<const bf16_t*>(residual); a.res_rs = res_stride;
   a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
   a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
-  const int strips = static_cast<int>((n + kStrip - 1) / kStrip);
-  a.KS = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, a.K);
+  a.KS = p.ks;
   const int steps = a.K / kStep;
   a.steps_per_split = (steps + a.KS - 1) / a.KS;
-  if (a.KS > 1 && !scratch) return HTN_EINVAL;
-  a.part = static_cast<float*>(scratch);
-  a.keys = static_cast<uint64_t*>(scratch);
+  void* tail = static_cast<char*>(scratch) + p.norm_bytes;
+  a.part = static_cast<float*>(tail);
+  a.keys = static_cast<uint64_t*>(tail);
   a.tokens = tokens;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool norm = gain != nullptr;
-  if (rows <= 16)
-    return norm ? dispatch_epi<1, true>(a, epilogue, st) : dispatch_epi<1, false>(a, epilogue, st);
-  return norm ? dispatch_epi<2, true>(a, epilogue, st) : dispatch_epi<2, false>(a, epilogue, st);
+  if (rows <= 16) return dispatch_epi<1>(a, epilogue, p.waves, st);
+  return dispatch_epi<2>(a, epilogue, p.waves, st);
 }

@@ -189,10 +189,11 @@ namespace {
 int norm_launch(bool add, const void* x, int64_t x_stride, const void* r, const void* gain,
                 void* summed, void* out, int64_t rows, int64_t cols, float eps,
                 htn_stream_t stream) {
-  if (!x || !gain || !out || rows <= 0 || cols <= 0 || cols > 8192 || x_stride < cols)
+  if (!x || !gain || !out || rows <= 0 || cols <= 0 || cols > 16384 || x_stride < cols)
     return HTN_EINVAL;
   if (add && (!r || !summed)) return HTN_EINVAL;
-  const bool vec = cols % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(gain) &&
+  // Rows past 8192 columns (beyond one wave's registers) take the scalar path.
+  const bool vec = cols <= 8192 && cols % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(gain) &&
                    aligned16(out) && (!add || (aligned16(r) && aligned16(summed)));
   const dim3 grid((rows + 3) / 4);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -106,15 +106,20 @@ class DraftSpeculator:
         with torch.inference_mode():
             current = self.prefill(prompt)
             yield [current]
-            emitted_count = 1
-            position = len(prompt)
+            yield from self.continue_from(current, len(prompt), max_new_tokens - 1)
+
+    def continue_from(self, current, position, count):
+        """Yield `count` more tokens after `current`, which sits at `position`
+        (both caches hold every earlier position)."""
+        with torch.inference_mode():
+            emitted_count = 0
             catch_up = None
-            while emitted_count < max_new_tokens:
+            while emitted_count < count:
                 emitted, proposal = self.cycle(current, position, catch_up)
                 all_accepted = len(emitted) == self.k + 1
                 catch_up = proposal[-1] if all_accepted else None
                 position += len(emitted)
-                for token in emitted[:max_new_tokens - emitted_count]:
+                for token in emitted[:count - emitted_count]:
                     emitted_count += 1
                     yield [token]
                 current = emitted[-1]

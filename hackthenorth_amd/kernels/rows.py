@@ -14,8 +14,8 @@ from .. import _lib
 MAX_ROWS = 32
 
 
-def _scratch(device, rows, n, k, epilogue):
-    nbytes = _lib.load().htn_gemm_rows_scratch_bytes(rows, n, k, epilogue)
+def _scratch(device, rows, n, k, epilogue, norm):
+    nbytes = _lib.load().htn_gemm_rows_scratch_bytes(rows, n, k, epilogue, int(norm))
     if nbytes <= 0:
         return None
     return torch.empty((nbytes + 7) // 8, dtype=torch.int64, device=device)
@@ -31,7 +31,7 @@ def _check(x, weight):
 
 def _launch(x, weight, n, epilogue, gain=None, eps=1e-6, residual=None, out=None, tokens=None):
     rows, k = x.shape
-    scratch = _scratch(x.device, rows, n, k, epilogue)
+    scratch = _scratch(x.device, rows, n, k, epilogue, gain is not None)
     _lib.call("htn_gemm_rows", _lib.ptr(x), x.stride(0), _lib.ptr(gain), float(eps),
               _lib.ptr(weight), n, k, rows, epilogue, _lib.ptr(residual),
               residual.stride(0) if residual is not None else 0, _lib.ptr(out),

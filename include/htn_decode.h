@@ -171,14 +171,15 @@ int htn_lm_head_argmax_w8(const void* x, const void* gain, float eps, const void
  *   x' = bf16(gain * bf16(x * rsqrt(mean(x^2) + eps))).
  * Epilogues (HTN_EPI_*): y[m, n] (row stride y_stride) as the batch-one GEMVs
  * round it, + residual[m, n] (row stride res_stride), SwiGLU, or tokens[m]
- * (int64 device array) = per-row argmax. k must be a multiple of 32, x
+ * (int64 device array) = per-row argmax. k must be a multiple of 64, x
  * (with its stride), gain and w 16-byte aligned.
- * scratch: htn_gemm_rows_scratch_bytes(rows, n, k, epilogue) bytes (K-split
- * partials or per-strip argmax keys; 0 means none is needed).
+ * scratch: htn_gemm_rows_scratch_bytes(rows, n, k, epilogue, gain != NULL)
+ * bytes (the normalised rows, K-split partials or per-strip argmax keys; 0
+ * means none is needed).
  * Replaces the reference's multi-row decode projections: Projection._tile
  * (projections.py:168-183), gate_up_swiglu (kernels/gateup.py:40-58) and the
  * split down projection (kernels/split_down.py:85-101). */
-int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue);
+int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue, int norm);
 int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps, const void* w,
                   int64_t n, int64_t k, int64_t rows, int epilogue, const void* residual,
                   int64_t res_stride, void* y, int64_t y_stride, int64_t* tokens, void* scratch,

@@ -34,7 +34,7 @@ def within_one_ulp(actual, expected):
     torch.testing.assert_close(a, e, atol=2e-2, rtol=2e-2)
 
 
-SHAPES = [(4096, 1024), (257, 2560), (40, 4096), (100, 12288), (1536, 9728), (3, 32)]
+SHAPES = [(4096, 1024), (257, 2560), (40, 4096), (100, 12288), (1536, 9728), (3, 64)]
 ROWS = [2, 5, 8, 16, 17, 32]
 
 
