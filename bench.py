@@ -355,6 +355,9 @@ def main():
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
+    ap.add_argument("--section", default="all",
+                    choices=("all", "qwen3-8b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative"),
+                    help="run one secondary workload alone and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the batch-one decode path on exactly one GPU; "
@@ -371,6 +374,20 @@ def main():
     def log(msg):
         if not args.quiet:
             print(msg, file=sys.stderr, flush=True)
+
+    if args.section != "all":
+        if args.section == "qwen3-8b":
+            r = run_decode("qwen3-8b", 2048, 256, args.warmup, log)
+            out = {k: r[k] for k in ("tok_s", "ms_per_step", "bytes_per_token", "decode_frac")}
+        elif args.section == "speculative":
+            out = run_draft_speculation(4096, 128, 4, log)
+        else:
+            fmt = "int8" if args.section.endswith("int8") else "fp8_e4m3"
+            r = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
+                           synthetic_context=True)
+            out = {k: r[k] for k in ("tok_s", "ms_per_step", "bytes_per_token", "decode_frac")}
+        print(json.dumps({"section": args.section, **out}), flush=True)
+        return
 
     res = run_decode("qwen3-0.6b", args.prompt, args.steps, args.warmup, log)
     log(f"qwen3-0.6b: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step")
