@@ -22,9 +22,10 @@ namespace htn {
 
 constexpr int D = HTN_HEAD_DIM;
 constexpr int kMaxRows = 32;        // G * Q
-constexpr int kSplit = 64;          // cache slots per block
+constexpr int kSplit = 64;          // cache slots per tile
+constexpr int kMinSplit = 16;       // fewest slots a block is given
 constexpr int kMaxQ = 8;            // queries per launch (verify rows)
-constexpr int kMergeUnroll = 8;     // partials loaded back to back in the merge
+constexpr int kMergeUnroll = 16;    // partials loaded back to back in the merge
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
 //   n = bf16(g * bf16(x * inv)); out_i = bf16(bf16(n_i cos_i) + bf16(rot(n)_i sin_i)).
@@ -153,7 +154,7 @@ struct AttnArgs {
   bf16_t* out;          // [B, Hq, Q, D]
   float* part;          // [B, Hq, Q, splits, D]
   float* ml;            // [B, Hq, Q, splits, 2]
-  int B, Hq, Hkv, G, Q, splits, split;
+  int B, Hq, Hkv, G, Q, splits, split, stream;
   float scale;
 };
 
@@ -177,15 +178,20 @@ enum Prologue { PRO_NONE = 0, PRO_ROW = 1, PRO_BY_POSITION = 2 };
 // K, then V; positions are scalar loads on their own counter. Every load is
 // unconditional: a branch that joins with fewer loads in flight, or a load
 // under a per-lane condition, makes the compiler wait for all of them.
-template <int ROWS, int PRO>
+//
+// TILES 64-slot tiles per block (2 when one tile per block would need more
+// blocks than fit on the GPU at once): all tiles' loads are issued up front
+// and the softmax spans the block's 64 * TILES slots.
+template <int ROWS, int PRO, int TILES>
 __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
+  constexpr int SPLIT = kSplit * TILES;
   constexpr int kQLoads = kMaxRows * (D / 2) / kBlock;  // q pairs per thread, unfused
   __shared__ uint32_t qs[kMaxRows * D / 2];  // query rows as bf16 pairs
-  __shared__ float sc[ROWS * kSplit];
+  __shared__ float sc[ROWS * SPLIT];
   __shared__ float accr[4 * ROWS * D];
   __shared__ float mrow[ROWS], lrow[ROWS];
-  __shared__ long rowpos[kMaxRows];  // absolute position of each query row
+  __shared__ int rowpos[kMaxRows];  // absolute position of each query row
   __shared__ __align__(16) bf16_t knew[D];
   __shared__ __align__(16) bf16_t vnew[D];
 
@@ -194,7 +200,9 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int rows = a.G * a.Q;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
-  const long start = static_cast<long>(s) * kSplit;
+  // The block owns slots [start, stop): a.split slots (at most SPLIT).
+  const int start = s * a.split;
+  const int stop = start + a.split < a.cap ? start + a.split : static_cast<int>(a.cap);
 
   // ---- 1. loads that gate the query rows.
   // Fused: 16 lanes per head slot, slots 0..G-1 the query heads, slot G the
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   if (PRO == PRO_ROW) head16_load(hsrc, is_k ? a.kg : a.qg, a.cos, a.sin, e, hq);
   // Unfused: the q rows (bf16 pairs) and each row's position, clamped reads.
   uint32_t qv[kQLoads];
-  long rpv = 0;
+  int rpv = 0;
   if (!FUSED) {
 #pragma unroll
     for (int i = 0; i < kQLoads; ++i) {
@@ -221,37 +229,44 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
           a.q + static_cast<long>(b) * a.q_sb + static_cast<long>(h) * a.q_sh +
           static_cast<long>(t) * a.q_st + d);
     }
-    rpv = a.pos[(tid < rows ? tid : 0) % a.Q];
+    rpv = static_cast<int>(a.pos[(tid < rows ? tid : 0) % a.Q]);
   }
 
-  // ---- 2. the split's K then V tiles (addresses from the block index only).
-  // Slots past the last position are masked below (scores -inf, V zeroed),
-  // so splits past it produce neutral partials with no branch.
-  const uint32_t row_bytes = static_cast<uint32_t>(a.cap) * D * 2;
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base, row_bytes);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base, row_bytes);
-  uint4 kreg[4];
-  uint32_t vreg[16];
-  const uint32_t koff = static_cast<uint32_t>(((start + wave * 4 + sub) * D + e * 8) * 2);
+  // ---- 2. the split's K then V tiles (addresses from the block index only),
+  // through descriptors over the block's range: slots past it read zeros
+  // without touching memory. Slots past the last position are masked below
+  // (scores -inf, V zeroed), so splits past it produce neutral partials with
+  // no branch.
+  const uint32_t range = stop > start ? static_cast<uint32_t>(stop - start) * D * 2 : 0u;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base + static_cast<long>(start) * D, range);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base + static_cast<long>(start) * D, range);
+  uint4 kreg[4 * TILES];
+  uint32_t vreg[16 * TILES];
+  const uint32_t koff = static_cast<uint32_t>(((wave * 4 + sub) * D + e * 8) * 2);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) kreg[u] = buffer_load16(krs, koff, u * 16 * D * 2);
-  const uint32_t voff = static_cast<uint32_t>(((start + wave * 16) * D + 2 * lane) * 2);
+  for (int u = 0; u < 4 * TILES; ++u) kreg[u] = buffer_load16(krs, koff, u * 16 * D * 2);
+  const uint32_t voff = static_cast<uint32_t>((wave * 16 * D + 2 * lane) * 2);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) vreg[i] = buffer_load4(vrs, voff + i * D * 2, 0);
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      vreg[t * 16 + i] = buffer_load4(vrs, voff + i * D * 2, t * kSplit * D * 2);
 
   // Positions: scalar loads of pos[min(t, Q - 1)] (in bounds, branch-free).
-  int64_t qp[kMaxQ];
-  int64_t maxpos = -1;
+  int qp[kMaxQ];
+  int maxpos = -1;
 #pragma unroll
   for (int t = 0; t < kMaxQ; ++t) {
     const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
-    qp[t] = t < a.Q ? v : -1;
+    // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
+    const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
+    qp[t] = t < a.Q ? vc : -1;
     maxpos = qp[t] > maxpos ? qp[t] : maxpos;
   }
-  if (maxpos >= a.cap) maxpos = a.cap - 1;
-  const long end = start + kSplit < maxpos + 1 ? start + kSplit : maxpos + 1;
+  if (maxpos >= a.cap) maxpos = static_cast<int>(a.cap) - 1;
+  const int end = stop < maxpos + 1 ? stop : maxpos + 1;
   const bool active = start <= maxpos;
-  const int64_t newest = FUSED ? qp[0] : -1;
+  const int newest = FUSED ? qp[0] : -1;
   const bool has_newest = FUSED && active && newest >= start && newest < end;
   if (PRO == PRO_BY_POSITION) {
     // The RoPE row needs the position: these loads queue behind K and V.
@@ -271,7 +286,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       qs[head_slot * (D / 2) + 32 + 2 * e] = ob.x;
       qs[head_slot * (D / 2) + 32 + 2 * e + 1] = ob.y;
     } else if (do_head) {
-      const long slot = kv_base + newest * D;
+      const long slot = kv_base + static_cast<long>(newest) * D;
       const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
       const uint2 va = *reinterpret_cast<const uint2*>(vsrc + 4 * e);
       const uint2 vb = *reinterpret_cast<const uint2*>(vsrc + 64 + 4 * e);
@@ -295,8 +310,8 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
     const uint4 kn = *reinterpret_cast<const uint4*>(knew + e * 8);
     const uint32_t vn = *reinterpret_cast<const uint32_t*>(vnew + 2 * lane);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const long j = start + u * 16 + wave * 4 + sub;
+    for (int u = 0; u < 4 * TILES; ++u) {
+      const int j = start + u * 16 + wave * 4 + sub;
       const bool hit = j == newest;
       kreg[u].x = hit ? kn.x : kreg[u].x;
       kreg[u].y = hit ? kn.y : kreg[u].y;
@@ -304,10 +319,12 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       kreg[u].w = hit ? kn.w : kreg[u].w;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const long j = start + wave * 16 + i;
-      vreg[i] = j == newest ? vn : vreg[i];
-    }
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int j = start + t * kSplit + wave * 16 + i;
+        vreg[t * 16 + i] = j == newest ? vn : vreg[t * 16 + i];
+      }
   }
 
   const int len = active ? static_cast<int>(end - start) : 0;
@@ -318,7 +335,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
     // ---- 4. scores q.k * D^-1/2. Rows past `rows` (when ROWS does not
     // divide it) compute on whatever their LDS rows hold and are never stored.
     uint32_t qr[ROWS][4];
-    long rp[ROWS];
+    int rp[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
 #pragma unroll
@@ -326,8 +343,8 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       rp[r] = rowpos[r0 + r];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const long j = start + u * 16 + wave * 4 + sub;
+    for (int u = 0; u < 4 * TILES; ++u) {
+      const int j = start + u * 16 + wave * 4 + sub;
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
         float dot = dot2(kreg[u].x, qr[r][0], 0.f);
@@ -335,18 +352,31 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
         dot = dot2(kreg[u].z, qr[r][2], dot);
         dot = dot2(kreg[u].w, qr[r][3], dot);
         const float dsum = row16_sum(dot);
-        if (e == 0 && j < end) sc[r * kSplit + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
+        if (e == 0 && j < end) sc[r * SPLIT + (j - start)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
       }
     }
     __syncthreads();
     // ---- 5. exact softmax numerators per row over this split
 #pragma unroll
     for (int r = wave; r < ROWS; r += 4) {
-      const float v = lane < len ? sc[r * kSplit + lane] : -INFINITY;
-      const float m = wave_max(v);
-      const float p = (lane < len && m != -INFINITY) ? expf(v - m) : 0.f;
-      sc[r * kSplit + lane] = p;
-      const float l = wave_sum(p);
+      float v[TILES];
+      float m = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int js = t * kSplit + lane;
+        v[t] = js < len ? sc[r * SPLIT + js] : -INFINITY;
+        m = fmaxf(m, v[t]);
+      }
+      m = wave_max(m);
+      float l = 0.f;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int js = t * kSplit + lane;
+        const float p = (js < len && m != -INFINITY) ? expf(v[t] - m) : 0.f;
+        sc[r * SPLIT + js] = p;
+        l += p;
+      }
+      l = wave_sum(l);
       if (lane == 0) {
         mrow[r] = m;
         lrow[r] = l;
@@ -357,13 +387,13 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
     // slots past the end carry p = 0 and a zeroed V row (the cache may hold
     // anything there, NaN included).
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int js = wave * 16 + i;
+    for (int i = 0; i < 16 * TILES; ++i) {
+      const int js = (i / 16) * kSplit + wave * 16 + (i % 16);
       const uint32_t vv = js < len ? vreg[i] : 0u;
       const float v0 = bf_lo(vv), v1 = bf_hi(vv);
 #pragma unroll
       for (int r = 0; r < ROWS; ++r) {
-        const float p = sc[r * kSplit + js];
+        const float p = sc[r * SPLIT + js];
         acc[r][0] = fmaf(p, v0, acc[r][0]);
         acc[r][1] = fmaf(p, v1, acc[r][1]);
       }
@@ -394,6 +424,265 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
       }
     }
     __syncthreads();
+  }
+}
+
+// Streaming split-KV attention for long contexts: a block owns T (even)
+// consecutive 64-slot tiles and keeps the next tile's K/V loads in flight
+// while it scores, normalises and accumulates the current one (online
+// softmax: running max and sum per row, accumulators rescaled per tile).
+// The buffer descriptors cover exactly the block's slot range, so tiles
+// past it read zeros without touching memory; loads stay unconditional.
+// Rows = G * Q must fit one chunk (<= ROWS). Query rows, positions and the
+// fused prologue are as in attention_partial.
+struct KVTile {
+  uint4 k[4];
+  uint32_t v[16];
+};
+
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                           uint32_t koff, uint32_t voff, int ti, KVTile& t) {
+  const uint32_t tb = static_cast<uint32_t>(ti) * kSplit * D * 2;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) t.k[u] = buffer_load16(krs, koff, tb + u * 16 * D * 2);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t.v[i] = buffer_load4(vrs, voff + i * D * 2, tb);
+}
+
+template <int ROWS>
+__device__ __forceinline__ void stream_tile(const AttnArgs& a, KVTile& t, int tbase, int tend,
+                                            bool has_newest, int newest, const uint4& kn,
+                                            uint32_t vn, const uint32_t (&qr)[ROWS][4],
+                                            const int (&rp)[ROWS], float* scb, float* mrun,
+                                            float* lrun, float* alph, float (&acc)[ROWS][2]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane >> 4, e = lane & 15;
+  if (has_newest && newest >= tbase && newest < tbase + kSplit) {  // block-uniform
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool hit = tbase + u * 16 + wave * 4 + sub == newest;
+      t.k[u].x = hit ? kn.x : t.k[u].x;
+      t.k[u].y = hit ? kn.y : t.k[u].y;
+      t.k[u].z = hit ? kn.z : t.k[u].z;
+      t.k[u].w = hit ? kn.w : t.k[u].w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t.v[i] = tbase + wave * 16 + i == newest ? vn : t.v[i];
+  }
+  // scores
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int j = tbase + u * 16 + wave * 4 + sub;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      float dot = dot2(t.k[u].x, qr[r][0], 0.f);
+      dot = dot2(t.k[u].y, qr[r][1], dot);
+      dot = dot2(t.k[u].z, qr[r][2], dot);
+      dot = dot2(t.k[u].w, qr[r][3], dot);
+      const float dsum = row16_sum(dot);
+      if (e == 0 && j < tend) scb[r * kSplit + (j - tbase)] = j <= rp[r] ? dsum * a.scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  // online softmax: wave w updates rows w, w + 4
+  const int lt = tend - tbase;
+  const int len = lt < 0 ? 0 : (lt > kSplit ? kSplit : lt);
+#pragma unroll
+  for (int r = wave; r < ROWS; r += 4) {
+    const float v = lane < len ? scb[r * kSplit + lane] : -INFINITY;
+    const float m_old = mrun[r];
+    const float m_new = fmaxf(m_old, wave_max(v));
+    const float alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+    const float p = (lane < len && m_new != -INFINITY) ? expf(v - m_new) : 0.f;
+    scb[r * kSplit + lane] = p;
+    const float l = wave_sum(p);
+    if (lane == 0) {
+      mrun[r] = m_new;
+      lrun[r] = fmaf(lrun[r], alpha, l);
+      alph[r] = alpha;
+    }
+  }
+  __syncthreads();
+  // P.V (slots past the end carry p = 0 and a zeroed V row)
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const float al = alph[r];
+    acc[r][0] *= al;
+    acc[r][1] *= al;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int js = wave * 16 + i;
+    const uint32_t vv = js < len ? t.v[i] : 0u;
+    const float v0 = bf_lo(vv), v1 = bf_hi(vv);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const float p = scb[r * kSplit + js];
+      acc[r][0] = fmaf(p, v0, acc[r][0]);
+      acc[r][1] = fmaf(p, v1, acc[r][1]);
+    }
+  }
+}
+
+template <int ROWS, int PRO>
+__global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
+  constexpr bool FUSED = PRO != PRO_NONE;
+  __shared__ uint32_t qs[kMaxRows * D / 2];
+  __shared__ float sc[2][ROWS * kSplit];
+  __shared__ float accr[4 * ROWS * D];
+  __shared__ float mrun[ROWS], lrun[ROWS], alph[ROWS];
+  __shared__ int rowpos[kMaxRows];
+  __shared__ __align__(16) bf16_t knew[D];
+  __shared__ __align__(16) bf16_t vnew[D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane >> 4, e = lane & 15;
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int rows = a.G * a.Q;
+  const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
+  const int start = s * a.split;
+  const int stop = start + a.split < a.cap ? start + a.split : static_cast<int>(a.cap);
+  const int ntiles = ((a.split + kSplit - 1) / kSplit + 1) & ~1;  // even
+
+  // ---- 1. loads that gate the query rows (as in attention_partial)
+  const int head_slot = wave * 4 + sub;
+  const bool is_k = head_slot == a.G;
+  const bf16_t* qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
+  const bf16_t* hsrc = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
+                            : qrow + (static_cast<long>(kvh) * a.G +
+                                      (head_slot < a.G ? head_slot : 0)) * D;
+  Head16 hq;
+  if (PRO == PRO_ROW) head16_load(hsrc, is_k ? a.kg : a.qg, a.cos, a.sin, e, hq);
+  uint32_t qv = 0;
+  int rpv = 0;
+  if (!FUSED) {
+    const int c = tid < rows * (D / 2) ? tid : 0;  // rows <= 4 here: one pair per thread
+    const int r = c / (D / 2), d = 2 * (c % (D / 2));
+    const int h = kvh * a.G + r / a.Q, tq = r % a.Q;
+    qv = *reinterpret_cast<const uint32_t*>(a.q + static_cast<long>(b) * a.q_sb +
+                                            static_cast<long>(h) * a.q_sh +
+                                            static_cast<long>(tq) * a.q_st + d);
+    rpv = static_cast<int>(a.pos[(tid < rows ? tid : 0) % a.Q]);
+  }
+
+  // ---- 2. the first two tiles of the block's range
+  const uint32_t range = stop > start ? static_cast<uint32_t>(stop - start) * D * 2 : 0u;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base + static_cast<long>(start) * D, range);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base + static_cast<long>(start) * D, range);
+  const uint32_t koff = static_cast<uint32_t>(((wave * 4 + sub) * D + e * 8) * 2);
+  const uint32_t voff = static_cast<uint32_t>((wave * 16 * D + 2 * lane) * 2);
+  KVTile ta, tb;
+  issue_tile(krs, vrs, koff, voff, 0, ta);
+  issue_tile(krs, vrs, koff, voff, 1, tb);
+
+  int qp[kMaxQ];
+  int maxpos = -1;
+#pragma unroll
+  for (int t = 0; t < kMaxQ; ++t) {
+    const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+    // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
+    const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
+    qp[t] = t < a.Q ? vc : -1;
+    maxpos = qp[t] > maxpos ? qp[t] : maxpos;
+  }
+  if (maxpos >= a.cap) maxpos = static_cast<int>(a.cap) - 1;
+  const int end = stop < maxpos + 1 ? stop : maxpos + 1;
+  const bool active = start <= maxpos;
+  const int newest = FUSED ? qp[0] : -1;
+  const bool has_newest = FUSED && active && newest >= start && newest < end;
+  if (PRO == PRO_BY_POSITION) {
+    const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
+    head16_load(hsrc, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
+  }
+
+  // ---- 3. query rows (and, fused, the newest k/v) into LDS
+  if (FUSED) {
+    const bool do_head = head_slot < a.G || (is_k && has_newest);
+    uint2 oa, ob;
+    head16_math(hq, is_k ? a.k_eps : a.q_eps, oa, ob);
+    if (tid < a.G) rowpos[tid] = newest;
+    if (do_head && !is_k) {
+      qs[head_slot * (D / 2) + 2 * e] = oa.x;
+      qs[head_slot * (D / 2) + 2 * e + 1] = oa.y;
+      qs[head_slot * (D / 2) + 32 + 2 * e] = ob.x;
+      qs[head_slot * (D / 2) + 32 + 2 * e + 1] = ob.y;
+    } else if (do_head) {
+      const long slot = kv_base + static_cast<long>(newest) * D;
+      const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
+      const uint2 va = *reinterpret_cast<const uint2*>(vsrc + 4 * e);
+      const uint2 vb = *reinterpret_cast<const uint2*>(vsrc + 64 + 4 * e);
+      *reinterpret_cast<uint2*>(knew + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(knew + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(vnew + 4 * e) = va;
+      *reinterpret_cast<uint2*>(vnew + 64 + 4 * e) = vb;
+      *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = va;
+      *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
+    }
+  } else {
+    if (tid < rows) rowpos[tid] = rpv;
+    if (tid < rows * (D / 2)) qs[tid] = qv;
+  }
+  if (tid < ROWS) {
+    mrun[tid] = -INFINITY;
+    lrun[tid] = 0.f;
+  }
+  __syncthreads();
+  uint4 kn = make_uint4(0, 0, 0, 0);
+  uint32_t vn = 0;
+  if (has_newest) {
+    kn = *reinterpret_cast<const uint4*>(knew + e * 8);
+    vn = *reinterpret_cast<const uint32_t*>(vnew + 2 * lane);
+  }
+  uint32_t qr[ROWS][4];
+  int rp[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qr[r][i] = qs[r * (D / 2) + e * 4 + i];
+    rp[r] = rowpos[r];
+  }
+  float acc[ROWS][2];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) acc[r][0] = acc[r][1] = 0.f;
+
+  // ---- 4. tiles, two per iteration, the next one always in flight (tiles
+  // past the block's range load nothing)
+#pragma unroll 1
+  for (int ti = 0; ti < ntiles; ti += 2) {
+    stream_tile<ROWS>(a, ta, start + ti * kSplit, end, has_newest, newest, kn, vn, qr, rp, sc[0],
+                      mrun, lrun, alph, acc);
+    issue_tile(krs, vrs, koff, voff, ti + 2, ta);
+    stream_tile<ROWS>(a, tb, start + (ti + 1) * kSplit, end, has_newest, newest, kn, vn, qr, rp,
+                      sc[1], mrun, lrun, alph, acc);
+    issue_tile(krs, vrs, koff, voff, ti + 3, tb);
+  }
+
+  // ---- 5. reduce the four waves' accumulators, write the partial (or the row)
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    accr[(wave * ROWS + r) * D + 2 * lane] = acc[r][0];
+    accr[(wave * ROWS + r) * D + 2 * lane + 1] = acc[r][1];
+  }
+  __syncthreads();
+  for (int i = tid; i < ROWS * D; i += kBlock) {
+    const int r = i / D, d = i % D;
+    if (r < rows) {
+      const float v = (accr[(0 * ROWS + r) * D + d] + accr[(1 * ROWS + r) * D + d]) +
+                      (accr[(2 * ROWS + r) * D + d] + accr[(3 * ROWS + r) * D + d]);
+      const int h = kvh * a.G + r / a.Q, tq = r % a.Q;
+      const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + tq;
+      if (a.splits == 1) {
+        a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrun[r]));
+      } else {
+        a.part[(orow * a.splits + s) * D + d] = v;
+        if (d == 0) {
+          a.ml[(orow * a.splits + s) * 2] = mrun[r];
+          a.ml[(orow * a.splits + s) * 2 + 1] = lrun[r];
+        }
+      }
+    }
   }
 }
 
@@ -469,15 +758,35 @@ using namespace htn;
 
 namespace {
 
-template <int ROWS>
-void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
+template <int ROWS, int TILES>
+void launch_partial_t(bool fused, const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.splits, a.Hkv, a.B);
   if (!fused)
-    hipLaunchKernelGGL((attention_partial<ROWS, PRO_NONE>), grid, dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_NONE, TILES>), grid, dim3(kBlock), 0, st, a);
   else if (a.rope_by_pos)
-    hipLaunchKernelGGL((attention_partial<ROWS, PRO_BY_POSITION>), grid, dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_BY_POSITION, TILES>), grid, dim3(kBlock), 0, st, a);
   else
-    hipLaunchKernelGGL((attention_partial<ROWS, PRO_ROW>), grid, dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((attention_partial<ROWS, PRO_ROW, TILES>), grid, dim3(kBlock), 0, st, a);
+}
+
+template <int ROWS>
+void launch_stream(bool fused, const AttnArgs& a, hipStream_t st) {
+  const dim3 grid(a.splits, a.Hkv, a.B);
+  if (!fused)
+    hipLaunchKernelGGL((attention_stream<ROWS, PRO_NONE>), grid, dim3(kBlock), 0, st, a);
+  else if (a.rope_by_pos)
+    hipLaunchKernelGGL((attention_stream<ROWS, PRO_BY_POSITION>), grid, dim3(kBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((attention_stream<ROWS, PRO_ROW>), grid, dim3(kBlock), 0, st, a);
+}
+
+template <int ROWS>
+void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
+  if constexpr (ROWS <= 4) {  // the streaming kernel when the plan chose it
+    if (a.stream) return launch_stream<ROWS>(fused, a, st);
+  }
+  if (a.split > kSplit) launch_partial_t<ROWS, 2>(fused, a, st);
+  else launch_partial_t<ROWS, 1>(fused, a, st);
 }
 
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
@@ -485,10 +794,33 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
     return HTN_EUNSUPPORTED;
   // One (batch, kv head) cache row is addressed with 32-bit byte offsets.
-  if (a.cap > (1L << 31) / (D * 2) - kSplit) return HTN_EUNSUPPORTED;
+  if (a.cap > (1L << 31) / (D * 2) - 2 * kSplit) return HTN_EUNSUPPORTED;
   if (fused && a.G + 1 > 16) return HTN_EUNSUPPORTED;  // 16 head slots in the fused prologue
-  a.split = kSplit;
-  a.splits = static_cast<int>((a.cap + kSplit - 1) / kSplit);
+  // Tiles per block: one while the GPU holds every block at once (about four
+  // per CU; a second residency round doubles the latency); past that, and
+  // when a block would own at least four tiles at about one block per CU, the
+  // streaming kernel with an even tile count (rows <= 4 per kv head).
+  // Slots per block. Short contexts: one 64-slot tile per block (more, smaller
+  // splits were measured slower: the merge grows); two tiles once one per
+  // block would need more blocks than fit on the GPU at once (about four per
+  // CU; a second residency round doubles the latency). Long contexts (rows <=
+  // 4 per kv head, at least four tiles per block at about one block per CU):
+  // the streaming kernel over an even number of tiles, ranges balanced.
+  const long tiles = (a.cap + kSplit - 1) / kSplit;
+  const long heads = static_cast<long>(a.Hkv) * a.B;
+  const long per_head = (device_cus() + heads - 1) / heads;
+  long split = kSplit;
+  a.stream = 0;
+  if (rows <= 4 && tiles >= 4 * per_head) {
+    const long t = 2 * (tiles / (2 * per_head));  // even tile count
+    const long nsplit = (a.cap + t * kSplit - 1) / (t * kSplit);
+    split = (a.cap + nsplit - 1) / nsplit;  // <= t tiles, balanced
+    a.stream = 1;
+  } else if (rows <= 8 && tiles * heads > 4L * device_cus()) {
+    split = 2 * kSplit;
+  }
+  a.split = static_cast<int>(split);
+  a.splits = static_cast<int>((a.cap + a.split - 1) / a.split);
   if (a.splits > 1 && !scratch) return HTN_EINVAL;
   const long nrow = static_cast<long>(a.B) * a.Hq * a.Q * a.splits;
   a.part = static_cast<float*>(scratch);
@@ -508,7 +840,8 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
 
 extern "C" int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap) {
   if (B <= 0 || Hq <= 0 || Q <= 0 || cap <= 0) return 0;
-  const long splits = (cap + kSplit - 1) / kSplit;
+  // The smallest split the plan picks is kMinSplit slots.
+  const long splits = (cap + kMinSplit - 1) / kMinSplit;
   return static_cast<long>(B) * Hq * Q * splits * (D + 2) * 4;
 }
 

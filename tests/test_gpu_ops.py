@@ -227,7 +227,9 @@ def test_grouped_attention_matches_oracle_and_ignores_unwritten_slots(batch, que
 
 @pytest.mark.parametrize("capacity,positions", [(257, (0, 63, 64, 256)),
                                                 (2080, (0, 511, 512, 2049)),
-                                                (640, (0, 1, 639))])
+                                                (640, (0, 1, 639)),
+                                                # two 64-slot tiles per block (1032 tiles of 8 heads)
+                                                (8200, (64, 127, 191, 8191))])
 def test_prologue_attention_matches_separate_ops_with_poisoned_tail(capacity, positions):
     # dryft/tests/test_fused_kernels.py:16-59 (batch one).
     qg, kg = _norm(nrm(40, (128,))), _norm(nrm(41, (128,)))
