@@ -81,6 +81,21 @@ __device__ __forceinline__ void head16_math(const Head16& h, float eps, uint2& o
   ob = make_uint2(pack_bf2(rb[0], rb[1]), pack_bf2(rb[2], rb[3]));
 }
 
+// Per-lane choice between two kernel arguments (q or k gain, q or k
+// epsilon). A plain select of two arguments is folded into a per-lane load of
+// the argument itself, a memory round trip ahead of the loads it addresses;
+// an opaque SGPR value in between keeps the arguments scalar. The gain is
+// reached as an offset from the q gain, so it stays a global address.
+__device__ __forceinline__ const bf16_t* pick_gain(const bf16_t* qg, const bf16_t* kg, bool k) {
+  long d = kg - qg;
+  asm("" : "+s"(d));
+  return qg + (k ? d : 0);
+}
+__device__ __forceinline__ float sgpr_f32(float f) {
+  asm("" : "+s"(f));
+  return f;
+}
+
 struct RopeArgs {
   const bf16_t* q; long q_sb, q_st;
   const bf16_t* k; long k_sb, k_st;
@@ -116,9 +131,9 @@ __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
   const bf16_t* src = is_q ? a.q + b * a.q_sb + t * a.q_st + h * D
                            : a.k + b * a.k_sb + t * a.k_st + h * D;
   Head16 hd;
-  head16_load(src, is_q ? a.qg : a.kg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hd);
+  head16_load(src, pick_gain(a.qg, a.kg, !is_q), a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hd);
   uint2 oa, ob;
-  head16_math(hd, is_q ? a.q_eps : a.k_eps, oa, ob);
+  head16_math(hd, is_q ? sgpr_f32(a.q_eps) : sgpr_f32(a.k_eps), oa, ob);
   if (!live || !rope_ok) return;
   if (is_q) {
     bf16_t* dst = a.out_q + ((b * a.T + t) * a.Hq + h) * D;
@@ -214,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
                             : qrow + (static_cast<long>(kvh) * a.G +
                                       (head_slot < a.G ? head_slot : 0)) * D;
   Head16 hq;
-  if (PRO == PRO_ROW) head16_load(hsrc, is_k ? a.kg : a.qg, a.cos, a.sin, e, hq);
+  if (PRO == PRO_ROW) head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos, a.sin, e, hq);
   // Unfused: the q rows (bf16 pairs) and each row's position, clamped reads.
   uint32_t qv[kQLoads];
   int rpv = 0;
@@ -271,14 +286,14 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   if (PRO == PRO_BY_POSITION) {
     // The RoPE row needs the position: these loads queue behind K and V.
     const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
-    head16_load(hsrc, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
+    head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
   }
 
   // ---- 3. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
     const bool do_head = head_slot < a.G || (is_k && has_newest);
     uint2 oa, ob;
-    head16_math(hq, is_k ? a.k_eps : a.q_eps, oa, ob);
+    head16_math(hq, is_k ? sgpr_f32(a.k_eps) : sgpr_f32(a.q_eps), oa, ob);
     if (tid < a.G) rowpos[tid] = newest;
     if (do_head && !is_k) {
       qs[head_slot * (D / 2) + 2 * e] = oa.x;
@@ -552,7 +567,7 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
                             : qrow + (static_cast<long>(kvh) * a.G +
                                       (head_slot < a.G ? head_slot : 0)) * D;
   Head16 hq;
-  if (PRO == PRO_ROW) head16_load(hsrc, is_k ? a.kg : a.qg, a.cos, a.sin, e, hq);
+  if (PRO == PRO_ROW) head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos, a.sin, e, hq);
   uint32_t qv = 0;
   int rpv = 0;
   if (!FUSED) {
@@ -592,14 +607,14 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
   const bool has_newest = FUSED && active && newest >= start && newest < end;
   if (PRO == PRO_BY_POSITION) {
     const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
-    head16_load(hsrc, is_k ? a.kg : a.qg, a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
+    head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hq);
   }
 
   // ---- 3. query rows (and, fused, the newest k/v) into LDS
   if (FUSED) {
     const bool do_head = head_slot < a.G || (is_k && has_newest);
     uint2 oa, ob;
-    head16_math(hq, is_k ? a.k_eps : a.q_eps, oa, ob);
+    head16_math(hq, is_k ? sgpr_f32(a.k_eps) : sgpr_f32(a.q_eps), oa, ob);
     if (tid < a.G) rowpos[tid] = newest;
     if (do_head && !is_k) {
       qs[head_slot * (D / 2) + 2 * e] = oa.x;

@@ -22,12 +22,14 @@ __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 (the rounding torch and the reference use).
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch and the reference use);
+// NaN stays NaN (quiet bit set). Both results are computed and selected, so the
+// conversion is straight-line code.
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = ((u >> 16) | 0x40u) & 0xffffu;
+  return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
 }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {

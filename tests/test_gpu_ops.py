@@ -205,7 +205,9 @@ def test_norm_rope_cache_matches_oracle_and_keeps_other_slots(batch, tokens):
 
 
 ATTN_CASES = [(1, 1, 0, 129), (1, 4, 63, 513), (4, 4, 126, 257), (1, 1, 2047, 2304),
-              (1, 5, 4091, 4100), (2, 1, 700, 8200)]
+              (1, 5, 4091, 4100), (2, 1, 700, 8200),
+              # one query per sequence: a tile boundary, batches, the last slot
+              (1, 1, 15, 129), (3, 1, 500, 513), (1, 1, 1023, 1024), (2, 1, 700, 1000)]
 
 
 @pytest.mark.parametrize("batch,queries,first,capacity", ATTN_CASES)
@@ -223,6 +225,22 @@ def test_grouped_attention_matches_oracle_and_ignores_unwritten_slots(batch, que
     vd[:, :, first + queries:] = float("nan")
     again = A.grouped_attention(qd, kd, vd, cuda(positions))
     assert bits_equal(again, actual.cpu())
+
+
+@pytest.mark.parametrize("heads,kv_heads,position,capacity",
+                         [(8, 8, 16, 40), (16, 8, 17, 600), (16, 8, 599, 600), (24, 8, 300, 301),
+                          (64, 8, 255, 1024), (16, 8, 1000, 1100)])
+def test_decode_attention_group_sizes_match_oracle(heads, kv_heads, position, capacity):
+    # One query per sequence over group sizes 1-8 (rows per kv head, 3 not a
+    # power of two); slots past the position hold NaN and must not be read.
+    q = nrm(33, (1, 1, heads, 128)).transpose(1, 2)
+    k, v = nrm(34, (1, kv_heads, capacity, 128)), nrm(35, (1, kv_heads, capacity, 128))
+    k[:, :, position + 1:] = float("nan")
+    v[:, :, position + 1:] = float("nan")
+    positions = torch.tensor([position])
+    actual = A.grouped_attention(cuda(q.contiguous()), cuda(k), cuda(v), cuda(positions))
+    expected = Q.attention(q, k, v, positions)
+    close(actual, expected)
 
 
 @pytest.mark.parametrize("capacity,positions", [(257, (0, 63, 64, 256)),
