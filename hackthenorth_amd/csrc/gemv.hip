@@ -136,24 +136,68 @@ __global__ __launch_bounds__(kBlock) void argmax_finish(const uint64_t* __restri
 
 // Weight batch: chunks c0 .. c0+U-1 of output rows n0 .. n0+R-1 (for SwiGLU
 // each is the pair gate row n, up row n + N). Lane l reads 16 bytes at vector
-// c*64 + l of each row; rows past the end re-read the last row (discarded).
+// c*64 + l of each row through a buffer descriptor over that row, so vectors
+// past the row's end read zeros without a per-lane branch; rows past the end
+// re-read the last row (discarded). n0 is wave-uniform. A batch that is not
+// `live` (past the wave's last row) gets empty descriptors: its loads return
+// zeros without touching memory, so the issue needs no branch.
 template <int R, int S, int U, int WF>
-__device__ __forceinline__ void issue_batch(const GemvArgs& a, long n0, int c0, int kv, int lane,
-                                            uint4 (&wv)[U][R][S]) {
+__device__ __forceinline__ void issue_batch(const GemvArgs& a, long n0, int c0, int lane,
+                                            bool live, uint4 (&wv)[U][R][S]) {
   const unsigned char* base = reinterpret_cast<const unsigned char*>(a.w);
+  const uint32_t row_bytes = static_cast<uint32_t>(a.k) * Fmt<WF>::kBytes;
+  const uint32_t range = live ? row_bytes : 0u;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const long n = n0 + r < a.n ? n0 + r : a.n - 1;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const unsigned char* row = base + (n + s * a.n) * static_cast<long>(a.k) * Fmt<WF>::kBytes;
+      const __amdgpu_buffer_rsrc_t rs =
+          buffer_rsrc(base + (n + s * a.n) * static_cast<long>(row_bytes), range);
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int v = (c0 + u) * 64 + lane;
-        wv[u][r][s] = v < kv ? load_stream(row + v * 16) : make_uint4(0, 0, 0, 0);
-      }
+      for (int u = 0; u < U; ++u)
+        wv[u][r][s] = buffer_load16_stream(rs, static_cast<uint32_t>(lane) * 16,
+                                           static_cast<uint32_t>(c0 + u) * 64 * 16);
     }
   }
+}
+
+// Per-row epilogue operands (8-bit row scales, the residual), loaded with the
+// row's first weight batch so the epilogue never waits on a fresh load.
+template <int R, int S, int EPI, int WF>
+__device__ __forceinline__ void issue_epilogue(const GemvArgs& a, long n0, float (&sc)[R][S],
+                                               float (&rs)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long n = n0 + r < a.n ? n0 + r : a.n - 1;
+    if constexpr (WF != WF_BF16) {
+      sc[r][0] = a.scale[n];
+      if (S > 1) sc[r][S - 1] = a.scale[n + a.n];
+    }
+    if constexpr (EPI == EPI_RESIDUAL) rs[r] = bf2f(a.res[n]);
+  }
+}
+
+// RMSNorm operands held in registers for rows up to kNormVecs * 8 * kBlock
+// elements (8192): each thread loads its x and gain vectors once.
+constexpr int kNormVecs = 4;
+
+// bf16(g * bf16(x * inv)) for eight packed elements (the reference's RMSNorm
+// roundings).
+__device__ __forceinline__ uint4 norm8(uint4 xv, uint4 gv, float inv) {
+  float f[8], g[8];
+  unpack8(xv, f);
+  unpack8(gv, g);
+  uint4 o;
+  o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+  o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+  o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+  o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+  return o;
+}
+
+__device__ __forceinline__ void pin4(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
 // One wave per output row (row pair for SwiGLU), rows grid-strided over
@@ -168,64 +212,116 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   __shared__ float red[kBlock / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
   bf16_t* xs = reinterpret_cast<bf16_t*>(smem);   // normalised x (NORM only)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform: readfirstlane keeps row addresses in SGPRs.
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kv = a.k / EPV;
   const int chunks = (kv + 63) >> 6;
   const long groups = (a.n + R - 1) / R;
   const long stride = static_cast<long>(gridDim.x) * 4;
   long grp = static_cast<long>(blockIdx.x) * 4 + wave;
+  const int kv8 = a.k >> 3;
+
+  // RMSNorm operands first: vector loads complete in issue order, so loading
+  // x and the gain ahead of the weights lets the prologue start as soon as
+  // they arrive instead of after the first weight batch.
+  // Every load before the first wait is unconditional: a branch that joins
+  // with fewer loads in flight makes the compiler wait for all of them.
+  uint4 xr[NORM ? kNormVecs : 1], gr[NORM ? kNormVecs : 1];
+  const bool norm_regs = NORM && a.k <= kNormVecs * 8 * kBlock;
+  if constexpr (NORM) {
+    const uint32_t bytes = static_cast<uint32_t>(a.k) * 2;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(a.x, bytes), grs = buffer_rsrc(a.gain, bytes);
+#pragma unroll
+    for (int i = 0; i < kNormVecs; ++i) {
+      xr[i] = buffer_load16(xrs, (threadIdx.x + i * kBlock) * 16, 0);
+      gr[i] = buffer_load16(grs, (threadIdx.x + i * kBlock) * 16, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weights
+  }
 
   // First weight batch before anything that waits on memory.
   uint4 wv[U][R][S];
-  bool pending = grp < groups;
-  if (pending) issue_batch<R, S, U, WF>(a, grp * R, 0, kv, lane, wv);
+  issue_batch<R, S, U, WF>(a, grp * R, 0, lane, grp < groups, wv);
 
   // RMSNorm prologue: the block normalises x once into LDS (bf16, rounded as
   // the reference rounds) and its waves then stream many rows against it.
   if constexpr (NORM) {
-    const int kv8 = a.k >> 3;
     float ss = 0.f;
-    for (int v = threadIdx.x; v < kv8; v += kBlock) {
-      float f[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
+    if (norm_regs) {
+      // The empty volatile asm keeps the arithmetic (and its wait) after the
+      // weight loads above.
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+      for (int i = 0; i < kNormVecs; ++i) {
+        pin4(xr[i]);
+        pin4(gr[i]);
+        float f[8];
+        unpack8(xr[i], f);  // vectors past the row read as zeros
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(f[j], f[j], ss);
+      }
+    } else {
+      for (int v = threadIdx.x; v < kv8; v += kBlock) {
+        float f[8];
+        unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+      }
     }
     const float inv = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(a.k) + a.eps);
-    for (int v = threadIdx.x; v < kv8; v += kBlock) {
-      float f[8], g[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.x + v * 8), f);
-      unpack8(*reinterpret_cast<const uint4*>(a.gain + v * 8), g);
-      uint4 o;
-      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
-      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
-      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
-      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
-      *reinterpret_cast<uint4*>(xs + v * 8) = o;
+    if (norm_regs) {
+#pragma unroll
+      for (int i = 0; i < kNormVecs; ++i) {
+        const int v = threadIdx.x + i * kBlock;
+        if (v < kv8) *reinterpret_cast<uint4*>(xs + v * 8) = norm8(xr[i], gr[i], inv);
+      }
+    } else {
+      for (int v = threadIdx.x; v < kv8; v += kBlock)
+        *reinterpret_cast<uint4*>(xs + v * 8) =
+            norm8(*reinterpret_cast<const uint4*>(a.x + v * 8),
+                  *reinterpret_cast<const uint4*>(a.gain + v * 8), inv);
     }
     __syncthreads();
   }
 
+  // Software pipeline: each wave keeps exactly one weight batch in flight.
+  // The batch after the one being multiplied (the row's next chunks, or the
+  // first chunks of the wave's next row) is issued right after the
+  // multiply, so it is in flight during the row's reduction and epilogue.
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(a.x, static_cast<uint32_t>(a.k) * 2);
   uint64_t best = 0;
   for (; grp < groups; grp += stride) {
     const long n0 = grp * R;
+    const long next = grp + stride;
+    // The row's epilogue operands, behind its first weight batch and ahead
+    // of the activations the multiply waits for.
+    float sc[R][S], rs[R];
+    issue_epilogue<R, S, EPI, WF>(a, n0, sc, rs);
     float acc[R][S];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int s = 0; s < S; ++s) acc[r][s] = 0.f;
-    for (int c0 = 0; c0 < chunks; c0 += U) {
-      if (!pending) issue_batch<R, S, U, WF>(a, n0, c0, kv, lane, wv);
-      pending = false;
+    // do-while: the compiler then knows a row issues loads after its
+    // epilogue operands, so the epilogue waits for those operands only.
+    int c0 = 0;
+    do {
       uint4 xv[U][EPV / 8];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int v = (c0 + u) * 64 + lane;
-        const bf16_t* src = NORM ? xs : a.x;
+        if constexpr (NORM) {
 #pragma unroll
-        for (int h = 0; h < EPV / 8; ++h)
-          xv[u][h] = v < kv ? *reinterpret_cast<const uint4*>(src + v * EPV + 8 * h)
-                            : make_uint4(0, 0, 0, 0);
+          for (int h = 0; h < EPV / 8; ++h)
+            xv[u][h] = v < kv ? *reinterpret_cast<const uint4*>(xs + v * EPV + 8 * h)
+                              : make_uint4(0, 0, 0, 0);
+        } else {
+          // Activations through a descriptor over x: vectors past the row
+          // read zeros (no per-lane branch).
+#pragma unroll
+          for (int h = 0; h < EPV / 8; ++h)
+            xv[u][h] = buffer_load16(xrs, static_cast<uint32_t>(v) * EPV * 2 + 16 * h, 0);
+        }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -242,7 +338,11 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
 #pragma unroll
           for (int s = 0; s < S; ++s) acc[r][s] = dot_vec<WF>(wv[u][r][s], xp, acc[r][s]);
       }
-    }
+      const bool last = c0 + U >= chunks;
+      const long ng = last ? next : grp;
+      issue_batch<R, S, U, WF>(a, ng * R, last ? 0 : c0 + U, lane, ng < groups, wv);
+      c0 += U;
+    } while (c0 < chunks);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const long n = n0 + r;
@@ -250,8 +350,8 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
       float t1 = S > 1 ? wave_sum(acc[r][S - 1]) : 0.f;
       if (n < a.n) {
         if (WF != WF_BF16) {
-          t0 *= a.scale[n];
-          if (S > 1) t1 *= a.scale[n + a.n];
+          t0 *= sc[r][0];
+          if (S > 1) t1 *= sc[r][S - 1];
         }
         if (EPI == EPI_ARGMAX) {
           const uint64_t key = argmax_key(f2bf(t0), static_cast<uint32_t>(n));
@@ -261,7 +361,7 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
           if (EPI == EPI_STORE) {
             out = t0;
           } else if (EPI == EPI_RESIDUAL) {
-            out = round_bf(t0) + bf2f(a.res[n]);
+            out = round_bf(t0) + rs[r];
           } else {
             out = silu_mul(round_bf(t0), round_bf(t1));
           }
