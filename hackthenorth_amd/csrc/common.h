@@ -22,18 +22,22 @@ __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 (the rounding torch and the reference use);
-// NaN stays NaN (quiet bit set). Both results are computed and selected, so the
-// conversion is straight-line code.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch and the reference
+// use). gfx950 converts in hardware (v_cvt_pk_bf16_f32): its results equal
+// the bit formula bf16 = (u + 0x7fff + ((u >> 16) & 1)) >> 16 on every normal,
+// subnormal, infinite and halfway input, and it keeps NaN payloads with the
+// quiet bit set ((u >> 16) | 0x40), as measured over 524288 bit patterns.
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t quiet = ((u >> 16) | 0x40u) & 0xffffu;
-  return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+// Two roundings in one v_cvt_pk_bf16_f32: lo in bits 0-15, hi in 16-31.
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return f2bf(lo) | (f2bf(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // 8 bf16 in a uint4 -> fp32 dot with 8 fp32 values.
@@ -61,8 +65,6 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // acc + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs (v_dot2c_f32_bf16:
 // the bf16 products are exact in fp32, accumulation in fp32).
