@@ -170,6 +170,7 @@ struct AttnArgs {
   float* part;          // [B, Hq, Q, splits, D]
   float* ml;            // [B, Hq, Q, splits, 2]
   int B, Hq, Hkv, G, Q, splits, split, stream;
+  int ring;             // LDS-staged kernel: tiles staged ahead (0: other kernels)
   float scale;
 };
 
@@ -701,6 +702,336 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
   }
 }
 
+// Decode attention with K/V staged through LDS (one query per sequence, up
+// to 8 query rows per kv head). A block owns `nt` consecutive 64-slot tiles;
+// each of its four waves owns 16 slots of every tile and loads exactly those
+// K and V rows straight into its own LDS region with 16-byte LDS-direct
+// buffer loads (no registers held while in flight), RING tiles ahead. A wave
+// then reads back only what it loaded itself and runs its own online
+// softmax, so the tile loop has no block barrier: lane (sub, e) holds dims
+// 8e..8e+7 of slots 4u + sub, a score is a 16-lane DPP row sum, the tile
+// maximum combines the four row groups with readlane, and P.V accumulates
+// per lane. The four wave states merge in LDS at the end into the block's
+// partial (or the output row when the block owns the whole cache).
+//
+// LDS-direct loads count on vmcnt like any vector load and complete in issue
+// order. The staging ring is read only through inline-asm ds_read with an
+// explicit vmcnt wait (the compiler would otherwise wait for every
+// outstanding LDS-direct load before each LDS read of that buffer), and the
+// block barriers are inline-asm s_barrier for the same reason; all other LDS
+// traffic uses separate static arrays.
+constexpr int kLdsWaveTile = 2 * 16 * D * 2;               // K + V bytes of one wave's 16 slots
+constexpr int kLdsTile = kLdsWaveTile * (kBlock / kWave);  // 32 KB per 64-slot tile
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// K then V of this wave's 16 slots of one tile: eight 1 KB LDS-direct loads.
+__device__ __forceinline__ void stage_tile(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                           unsigned char* wave_lds, int lane, uint32_t tile_off) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(wave_lds + u * 1024), 16, lane * 16,
+                                             tile_off + u * 1024, 0, 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(wave_lds + 4096 + u * 1024), 16,
+                                             lane * 16, tile_off + u * 1024, 0, 0);
+}
+
+// Wait until at most WAIT vector-memory operations are outstanding, then
+// read this lane's 16 bytes of K and V for the four slot quads.
+template <int WAIT>
+__device__ __forceinline__ void read_tile(uint32_t addr, uint4 (&ko)[4], uint4 (&vo)[4]) {
+  u32x4 k[4], v[4];
+  asm volatile(
+      "s_waitcnt vmcnt(%8)\n\t"
+      "ds_read_b128 %0, %9\n\t"
+      "ds_read_b128 %1, %9 offset:1024\n\t"
+      "ds_read_b128 %2, %9 offset:2048\n\t"
+      "ds_read_b128 %3, %9 offset:3072\n\t"
+      "ds_read_b128 %4, %9 offset:4096\n\t"
+      "ds_read_b128 %5, %9 offset:5120\n\t"
+      "ds_read_b128 %6, %9 offset:6144\n\t"
+      "ds_read_b128 %7, %9 offset:7168\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      // early-clobber outputs: a destination must never share the address
+      // register, which the later reads of the sequence still use
+      : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+        "=&v"(v[2]), "=&v"(v[3])
+      : "n"(WAIT), "v"(addr)
+      : "memory");
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ko[i] = make_uint4(k[i].x, k[i].y, k[i].z, k[i].w);
+    vo[i] = make_uint4(v[i].x, v[i].y, v[i].z, v[i].w);
+  }
+}
+
+template <int ROWS, int PRO, int RING>
+__global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
+  constexpr bool FUSED = PRO != PRO_NONE;
+  extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  __shared__ uint32_t qs[ROWS * D / 2];
+  __shared__ float wm[kBlock / kWave][ROWS], wl[kBlock / kWave][ROWS];
+  __shared__ float wacc[kBlock / kWave][ROWS][D];
+  __shared__ __align__(16) bf16_t knew[D];
+  __shared__ __align__(16) bf16_t vnew[D];
+
+  // The wave index is uniform: readfirstlane keeps LDS and tile offsets scalar.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane >> 4, e = lane & 15;
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int rows = a.G;
+  const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
+  const int start = s * a.split;
+  const int stop = start + a.split < a.cap ? start + a.split : static_cast<int>(a.cap);
+  const int nt = (a.split + kSplit - 1) / kSplit;
+
+  // ---- 1. loads that gate the query rows (as in attention_partial), the
+  // newest v row, then the position.
+  const int head_slot = wave * 4 + sub;
+  const bool is_k = head_slot == a.G;
+  const bf16_t* qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
+  const bf16_t* hsrc = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
+                            : qrow + (static_cast<long>(kvh) * a.G +
+                                      (head_slot < a.G ? head_slot : 0)) * D;
+  Head16 hq;
+  uint2 va = make_uint2(0, 0), vb = make_uint2(0, 0);
+  if (PRO == PRO_ROW) head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos, a.sin, e, hq);
+  if (FUSED) {
+    const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
+    va = *reinterpret_cast<const uint2*>(vsrc + 4 * e);
+    vb = *reinterpret_cast<const uint2*>(vsrc + 64 + 4 * e);
+  }
+  constexpr int kQL = (ROWS * (D / 2) + kBlock - 1) / kBlock;  // q pairs per thread
+  uint32_t qv[kQL];
+  if (!FUSED) {
+#pragma unroll
+    for (int j = 0; j < kQL; ++j) {
+      const int idx = tid + j * kBlock;
+      const int c = idx < rows * (D / 2) ? idx : 0;
+      const int h = kvh * a.G + c / (D / 2), d = 2 * (c % (D / 2));
+      qv[j] = *reinterpret_cast<const uint32_t*>(a.q + static_cast<long>(b) * a.q_sb +
+                                                 static_cast<long>(h) * a.q_sh + d);
+    }
+  }
+  // ---- 2. stage the first RING tiles at once, through descriptors over the
+  // block's slots up to the capacity (slots past the newest position are
+  // masked below); later tiles use descriptors over the visible slots only,
+  // which read as zeros past them without touching memory.
+  const uint32_t cap_range = static_cast<uint32_t>(stop - start) * D * 2;
+  const bf16_t* kb = a.keys + kv_base + static_cast<long>(start) * D;
+  const bf16_t* vb0 = a.values + kv_base + static_cast<long>(start) * D;
+  unsigned char* wave_ring = ring + wave * kLdsWaveTile;
+  const uint32_t wave_off = static_cast<uint32_t>(wave) * 16 * D * 2;  // this wave's 16 slots
+  {
+    const __amdgpu_buffer_rsrc_t krs0 = buffer_rsrc(kb, cap_range);
+    const __amdgpu_buffer_rsrc_t vrs0 = buffer_rsrc(vb0, cap_range);
+#pragma unroll
+    for (int t = 0; t < RING; ++t)
+      stage_tile(krs0, vrs0, wave_ring + t * kLdsTile, lane, t * kSplit * D * 2 + wave_off);
+  }
+  const int64_t pv = a.pos[0];
+  const int pos = pv < 0 ? -1 : (pv >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(pv));
+  const int last = pos < a.cap ? pos : static_cast<int>(a.cap) - 1;
+  const int end = stop < last + 1 ? stop : last + 1;  // slots [start, end) are visible
+  const int newest = FUSED && pos >= 0 && pos < a.cap ? pos : -1;
+  const bool has_newest = newest >= start && newest < end;
+  if (PRO == PRO_BY_POSITION) {
+    const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
+    head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos + ri * a.rope_st,
+                a.sin + ri * a.rope_st, e, hq);
+  }
+
+  const uint32_t range = end > start ? static_cast<uint32_t>(end - start) * D * 2 : 0u;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kb, range);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vb0, range);
+
+  // ---- 3. query rows (and, fused, the newest k/v) into LDS
+  if (FUSED) {
+    const bool do_head = head_slot < a.G || (is_k && has_newest);
+    uint2 oa, ob;
+    head16_math(hq, is_k ? sgpr_f32(a.k_eps) : sgpr_f32(a.q_eps), oa, ob);
+    if (do_head && !is_k) {
+      qs[head_slot * (D / 2) + 2 * e] = oa.x;
+      qs[head_slot * (D / 2) + 2 * e + 1] = oa.y;
+      qs[head_slot * (D / 2) + 32 + 2 * e] = ob.x;
+      qs[head_slot * (D / 2) + 32 + 2 * e + 1] = ob.y;
+    } else if (do_head) {
+      const long slot = kv_base + static_cast<long>(newest) * D;
+      *reinterpret_cast<uint2*>(knew + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(knew + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(vnew + 4 * e) = va;
+      *reinterpret_cast<uint2*>(vnew + 64 + 4 * e) = vb;
+      *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = va;
+      *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kQL; ++j)
+      if (tid + j * kBlock < rows * (D / 2)) qs[tid + j * kBlock] = qv[j];
+  }
+  lds_barrier();
+  uint4 kn = make_uint4(0, 0, 0, 0), vn = make_uint4(0, 0, 0, 0);
+  if (has_newest) {
+    kn = *reinterpret_cast<const uint4*>(knew + e * 8);
+    vn = *reinterpret_cast<const uint4*>(vnew + e * 8);
+  }
+  // Rows past G (ROWS rounds G up) score row 0 and are never stored.
+  uint32_t qr[ROWS][4];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const int rr = r < rows ? r : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qr[r][i] = qs[rr * (D / 2) + e * 4 + i];
+  }
+  const float scale2 = a.scale * 1.4426950408889634f;  // log2(e) / sqrt(D)
+  float m[ROWS], l[ROWS], acc[ROWS][8];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[r][i] = 0.f;
+  }
+
+  // ---- 4. tiles: wait for this wave's staged rows of tile t (the tiles
+  // staged after it may stay in flight), score, online softmax, P.V, then
+  // stage tile t + RING into the slot just read.
+  const uint32_t lane_addr =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(wave_ring))) + lane * 16;
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    const int q = t % RING;
+    uint4 kt[4], vt[4];
+    const int later = nt - 1 - t < RING - 1 ? nt - 1 - t : RING - 1;  // tiles staged after t
+    const uint32_t at = lane_addr + q * kLdsTile;
+    if (RING == 1 || later == 0) read_tile<0>(at, kt, vt);
+    else if (RING == 2 || later == 1) read_tile<8>(at, kt, vt);
+    else if (later == 2) read_tile<16>(at, kt, vt);
+    else read_tile<24>(at, kt, vt);
+    const int tbase = start + t * kSplit + wave * 16;  // this wave's first slot
+    if (has_newest && newest >= tbase && newest < tbase + 16) {  // wave-uniform
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool hit = tbase + 4 * u + sub == newest;
+        kt[u].x = hit ? kn.x : kt[u].x; kt[u].y = hit ? kn.y : kt[u].y;
+        kt[u].z = hit ? kn.z : kt[u].z; kt[u].w = hit ? kn.w : kt[u].w;
+        vt[u].x = hit ? vn.x : vt[u].x; vt[u].y = hit ? vn.y : vt[u].y;
+        vt[u].z = hit ? vn.z : vt[u].z; vt[u].w = hit ? vn.w : vt[u].w;
+      }
+    }
+    // Scores live in the base-2 domain (q.k * log2(e) / sqrt(D)) so each
+    // weight is one v_exp_f32; masks are only applied on the tile that
+    // crosses the end of the visible slots.
+    const bool full = tbase + 16 <= end;  // wave-uniform
+    float vf[4][8];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ok[u] = full || tbase + 4 * u + sub < end;
+      unpack8(vt[u], vf[u]);
+    }
+    if (!full) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[u][i] = ok[u] ? vf[u][i] : 0.f;  // never NaN * 0
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      float sc[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float dot = dot2(kt[u].x, qr[r][0], 0.f);
+        dot = dot2(kt[u].y, qr[r][1], dot);
+        dot = dot2(kt[u].z, qr[r][2], dot);
+        dot = dot2(kt[u].w, qr[r][3], dot);
+        const float dsum = row16_sum(dot);
+        sc[u] = ok[u] ? dsum * scale2 : -INFINITY;
+        tmax = fmaxf(tmax, sc[u]);
+      }
+      tmax = fmaxf(fmaxf(readlane(tmax, 0), readlane(tmax, 16)),
+                   fmaxf(readlane(tmax, 32), readlane(tmax, 48)));
+      const float m_new = fmaxf(m[r], tmax);
+      if (m_new != -INFINITY) {  // wave-uniform
+        // exp2(-inf) is 0: a first tile (m = -inf) or a masked slot weighs 0
+        const float alpha = __builtin_amdgcn_exp2f(m[r] - m_new);
+        m[r] = m_new;
+        float ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r][i] *= alpha;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float pu = __builtin_amdgcn_exp2f(sc[u] - m_new);
+          ls += pu;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[r][i] = fmaf(pu, vf[u][i], acc[r][i]);
+        }
+        l[r] = fmaf(l[r], alpha, ls);
+      }
+    }
+    const int tn = t + RING;
+    if (tn < nt)  // wave-uniform
+      stage_tile(krs, vrs, wave_ring + q * kLdsTile, lane, tn * kSplit * D * 2 + wave_off);
+  }
+  // Every staging load has landed before the block's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- 5. sum the four row groups (same dims, different slots), merge the
+  // waves' states in LDS, write the block's partial (or the rows).
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc[r][i] += __shfl_xor(acc[r][i], 16, kWave);
+      acc[r][i] += __shfl_xor(acc[r][i], 32, kWave);
+    }
+    // every lane of a row group holds that group's sum
+    const float lw =
+        (readlane(l[r], 0) + readlane(l[r], 16)) + (readlane(l[r], 32) + readlane(l[r], 48));
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wacc[wave][r][8 * e + i] = acc[r][i];
+    }
+    if (lane == 0) {
+      wm[wave][r] = m[r];
+      wl[wave][r] = lw;
+    }
+  }
+  lds_barrier();
+  for (int i = tid; i < rows * D; i += kBlock) {
+    const int r = i / D, d = i % D;
+    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+      const float f = wm[w][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][r] - M);
+      num = fmaf(f, wacc[w][r][d], num);
+      den = fmaf(f, wl[w][r], den);
+    }
+    const long orow = static_cast<long>(b) * a.Hq + kvh * a.G + r;
+    if (a.splits == 1) {
+      a.out[orow * D + d] = static_cast<bf16_t>(f2bf(num / den));
+    } else {
+      a.part[(orow * a.splits + s) * D + d] = num;
+      if (d == 0) {
+        // the merge weighs partials with natural exponentials: max back to base e
+        a.ml[(orow * a.splits + s) * 2] = M * 0.6931471805599453f;
+        a.ml[(orow * a.splits + s) * 2 + 1] = den;
+      }
+    }
+  }
+}
+
 // Merge of the split partials, one block per output row (b, h, t):
 //   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
 // Each wave folds every fourth split with an online max (one pass over the
@@ -795,8 +1126,33 @@ void launch_stream(bool fused, const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attention_stream<ROWS, PRO_ROW>), grid, dim3(kBlock), 0, st, a);
 }
 
+template <int ROWS, int PRO, int RING>
+void launch_lds_t(const AttnArgs& a, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(RING) * kLdsTile;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&attention_lds<ROWS, PRO, RING>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  (void)attr;  // a refused size surfaces as a launch error
+  hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING>), dim3(a.splits, a.Hkv, a.B), dim3(kBlock),
+                     lds, st, a);
+}
+
+template <int ROWS, int PRO>
+void launch_lds_p(const AttnArgs& a, hipStream_t st) {
+  if (a.ring == 1) launch_lds_t<ROWS, PRO, 1>(a, st);
+  else if (a.ring == 2) launch_lds_t<ROWS, PRO, 2>(a, st);
+  else launch_lds_t<ROWS, PRO, 4>(a, st);
+}
+
 template <int ROWS>
 void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
+  if constexpr (ROWS <= 8) {  // the LDS-staged kernel when the plan chose it
+    if (a.ring) {
+      if (!fused) return launch_lds_p<ROWS, PRO_NONE>(a, st);
+      if (a.rope_by_pos) return launch_lds_p<ROWS, PRO_BY_POSITION>(a, st);
+      return launch_lds_p<ROWS, PRO_ROW>(a, st);
+    }
+  }
   if constexpr (ROWS <= 4) {  // the streaming kernel when the plan chose it
     if (a.stream) return launch_stream<ROWS>(fused, a, st);
   }
@@ -811,27 +1167,40 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   // One (batch, kv head) cache row is addressed with 32-bit byte offsets.
   if (a.cap > (1L << 31) / (D * 2) - 2 * kSplit) return HTN_EUNSUPPORTED;
   if (fused && a.G + 1 > 16) return HTN_EUNSUPPORTED;  // 16 head slots in the fused prologue
-  // Tiles per block: one while the GPU holds every block at once (about four
-  // per CU; a second residency round doubles the latency); past that, and
-  // when a block would own at least four tiles at about one block per CU, the
-  // streaming kernel with an even tile count (rows <= 4 per kv head).
-  // Slots per block. Short contexts: one 64-slot tile per block (more, smaller
+  // One query per sequence (decode): the LDS-staged kernel. One 64-slot
+  // tile per block while the blocks fit two per CU; past that, just enough
+  // tiles per block to keep the grid within one block per CU (all blocks
+  // resident at once; a second residency round doubles the time), with two
+  // or four tiles staged ahead.
+  // Several queries (verify rows): one 64-slot tile per block (more, smaller
   // splits were measured slower: the merge grows); two tiles once one per
   // block would need more blocks than fit on the GPU at once (about four per
-  // CU; a second residency round doubles the latency). Long contexts (rows <=
-  // 4 per kv head, at least four tiles per block at about one block per CU):
-  // the streaming kernel over an even number of tiles, ranges balanced.
+  // CU). Long contexts (rows <= 4 per kv head, at least four tiles per block
+  // at about one block per CU): the streaming kernel over an even number of
+  // tiles, ranges balanced.
   const long tiles = (a.cap + kSplit - 1) / kSplit;
   const long heads = static_cast<long>(a.Hkv) * a.B;
-  const long per_head = (device_cus() + heads - 1) / heads;
+  const long cus = device_cus();
+  const long per_head = (cus + heads - 1) / heads;
   long split = kSplit;
   a.stream = 0;
-  if (rows <= 4 && tiles >= 4 * per_head) {
+  a.ring = 0;
+  if (a.Q == 1 && rows <= 8 && (heads * tiles <= cus || heads * tiles > 2 * cus)) {
+    // LDS per block: 32 KB per staged tile plus up to 19 KB (8 rows) of
+    // state; two-tile rings fit two blocks per CU for rows <= 4. Between one
+    // and two single-tile blocks per CU the register kernel below was
+    // measured faster (8B shape, 2K context).
+    const long per_cu = rows <= 4 ? 2 : 1;
+    long nt = 1;
+    if (heads * tiles > 2 * cus) nt = (heads * tiles + per_cu * cus - 1) / (per_cu * cus);
+    a.ring = nt == 1 ? 1 : (per_cu == 2 || nt < 4 ? 2 : 4);
+    split = nt * kSplit;
+  } else if (rows <= 4 && tiles >= 4 * per_head) {
     const long t = 2 * (tiles / (2 * per_head));  // even tile count
     const long nsplit = (a.cap + t * kSplit - 1) / (t * kSplit);
     split = (a.cap + nsplit - 1) / nsplit;  // <= t tiles, balanced
     a.stream = 1;
-  } else if (rows <= 8 && tiles * heads > 4L * device_cus()) {
+  } else if (rows <= 8 && tiles * heads > 4L * cus) {
     split = 2 * kSplit;
   }
   a.split = static_cast<int>(split);
