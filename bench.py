@@ -72,7 +72,7 @@ def kv_bytes_per_token(cfg, ctx):
 
 
 def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
-               synthetic_context=False):
+               synthetic_context=False, batch=1, model=None):
     """Greedy decode of `steps` tokens after a prompt of `prompt_len` tokens.
 
     synthetic_context: instead of prefilling, fill every KV slot with N(0,1)
@@ -80,16 +80,17 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
     depend on the cached values; this keeps 8192-token contexts cheap to set up).
     """
     cfg = shape_config(shape, weight_format=weight_format)
-    model = Qwen3Model.random(cfg)
+    if model is None:
+        model = Qwen3Model.random(cfg)
     prompt = DR.randint(prompt_len, cfg.vocab_size, PROMPT_SEED, PROMPT_STREAM)
     total = warmup + steps + 1
     with torch.inference_mode():
-        state = D.DecodeState(model, 1, prompt_len, total)
+        state = D.DecodeState(model, batch, prompt_len, total)
         t0 = time.perf_counter()
         if synthetic_context:
             DR.normal_(state.cache.storage.view(-1), 21, 77, 1.0)
             state.position.fill_(prompt_len)
-            state.token.copy_(prompt[-1:].view(1, 1))
+            state.token.copy_(prompt[-batch:].view(batch, 1))
             first = state.token.clone()
             log(f"{shape} {weight_format}: synthetic {prompt_len}-slot KV cache")
         else:
@@ -102,7 +103,7 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
         # Time exactly `steps` decode steps from the state right after prefill.
         state.position.fill_(prompt_len)
         state.token.copy_(first)
-        tokens = torch.empty(steps, dtype=torch.int64, device=model.device)
+        tokens = torch.empty((steps, batch), dtype=torch.int64, device=model.device)
         torch.cuda.synchronize()
         start = time.perf_counter()
         for i in range(steps):
@@ -114,15 +115,35 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
         state.token.copy_(first)
         for i in range(steps):
             state.graph.replay()
-            tokens[i:i + 1].copy_(state.token[0])
+            tokens[i].copy_(state.token[:, 0])
         torch.cuda.synchronize()
     mean_ctx = prompt_len + (steps - 1) / 2.0
-    bytes_per_token = model.decode_weight_bytes() + kv_bytes_per_token(cfg, mean_ctx)
-    tok_s = steps / elapsed
-    return dict(model=model, cfg=cfg, prompt=prompt.cpu().tolist(), first=int(first),
-                tokens=tokens.cpu().tolist(), elapsed=elapsed, tok_s=tok_s,
+    # Bytes per step: every weight once, each sequence's KV; per token at batch one.
+    bytes_per_token = (model.decode_weight_bytes() + batch * kv_bytes_per_token(cfg, mean_ctx)) / batch
+    tok_s = batch * steps / elapsed
+    toks = tokens.cpu()
+    return dict(model=model, cfg=cfg, prompt=prompt.cpu().tolist(), first=int(first[0, 0]),
+                tokens=(toks[:, 0] if batch == 1 else toks).tolist(), elapsed=elapsed, tok_s=tok_s,
                 ms_per_step=1e3 * elapsed / steps, bytes_per_token=bytes_per_token,
                 decode_frac=bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9))
+
+
+def run_batched(shape, ctx, steps, batches, log):
+    """Batched greedy decode (B sequences per captured step, synthetic KV at
+    context `ctx`): aggregate tok/s per batch size, one model for all."""
+    model = Qwen3Model.random(shape_config(shape))
+    out = {"workload": f"{shape} bf16 batched greedy decode, {steps} steps at context {ctx} "
+                       "(synthetic N(0,1) KV), one captured HIP graph per step: multi-row MFMA "
+                       "projections and per-sequence attention", "by_batch": {}}
+    for b in batches:
+        r = run_decode(shape, ctx, steps, 2, log, synthetic_context=True, batch=b, model=model)
+        out["by_batch"][str(b)] = {"tok_s": round(r["tok_s"], 1),
+                                   "ms_per_step": round(r["ms_per_step"], 4),
+                                   "per_sequence_tok_s": round(r["tok_s"] / b, 1)}
+        log(f"{shape} batch {b}: {r['tok_s']:.1f} tok/s aggregate, {r['ms_per_step']:.3f} ms/step")
+        del r
+        torch.cuda.empty_cache()
+    return out
 
 
 def graph_ms(graph, reps=20):
@@ -356,7 +377,8 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
-                    choices=("all", "qwen3-8b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative"),
+                    choices=("all", "qwen3-8b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
+                             "batched"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -381,6 +403,8 @@ def main():
             out = {k: r[k] for k in ("tok_s", "ms_per_step", "bytes_per_token", "decode_frac")}
         elif args.section == "speculative":
             out = run_draft_speculation(4096, 128, 4, log)
+        elif args.section == "batched":
+            out = run_batched("qwen3-8b", 512, 32, (1, 4, 16), log)
         else:
             fmt = "int8" if args.section.endswith("int8") else "fp8_e4m3"
             r = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
@@ -456,6 +480,11 @@ def main():
             line["speculative_4b_draft_0.6b"] = run_draft_speculation(4096, 128, 4, log)
         except Exception as exc:
             line["speculative_4b_draft_0.6b"] = {"error": repr(exc)}
+        torch.cuda.empty_cache()
+        try:
+            line["batched_qwen3_8b"] = run_batched("qwen3-8b", 512, 32, (4, 16), log)
+        except Exception as exc:
+            line["batched_qwen3_8b"] = {"error": repr(exc)}
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(res["prompt"], res["tokens"], res["first"])

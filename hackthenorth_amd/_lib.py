@@ -55,7 +55,7 @@ SIGNATURES = {
                             _I64, _I64, _P],
     "htn_attention_scratch_bytes": [_I64, _I64, _I64, _I64],
     "htn_grouped_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
-                              _I64, _P, _P],
+                              _I64, _I64, _I64, _I64, _P, _P],
     "htn_prologue_attention": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64, _I,
                                _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P],
 }

@@ -166,7 +166,8 @@ struct AttnArgs {
   const bf16_t* cos; const bf16_t* sin; long rope_st, rope_rows; int rope_by_pos;
   bf16_t* keys; bf16_t* values; long cap;
   const int64_t* pos;
-  bf16_t* out;          // [B, Hq, Q, D]
+  bf16_t* out;          // row (b, h, t) at b*o_sb + h*o_sh + t*o_st (dims contiguous)
+  long o_sb, o_sh, o_st;
   float* part;          // [B, Hq, Q, splits, D]
   float* ml;            // [B, Hq, Q, splits, 2]
   int B, Hq, Hkv, G, Q, splits, split, stream;
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
         const int h = kvh * a.G + rr / a.Q, t = rr % a.Q;
         const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
         if (a.splits == 1) {
-          a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrow[r]));
+          a.out[b * a.o_sb + h * a.o_sh + t * a.o_st + d] = static_cast<bf16_t>(f2bf(v / lrow[r]));
         } else {
           a.part[(orow * a.splits + s) * D + d] = v;
           if (d == 0) {
@@ -690,7 +691,7 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
       const int h = kvh * a.G + r / a.Q, tq = r % a.Q;
       const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + tq;
       if (a.splits == 1) {
-        a.out[orow * D + d] = static_cast<bf16_t>(f2bf(v / lrun[r]));
+        a.out[b * a.o_sb + h * a.o_sh + tq * a.o_st + d] = static_cast<bf16_t>(f2bf(v / lrun[r]));
       } else {
         a.part[(orow * a.splits + s) * D + d] = v;
         if (d == 0) {
@@ -1020,7 +1021,7 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
     }
     const long orow = static_cast<long>(b) * a.Hq + kvh * a.G + r;
     if (a.splits == 1) {
-      a.out[orow * D + d] = static_cast<bf16_t>(f2bf(num / den));
+      a.out[b * a.o_sb + (kvh * a.G + r) * a.o_sh + d] = static_cast<bf16_t>(f2bf(num / den));
     } else {
       a.part[(orow * a.splits + s) * D + d] = num;
       if (d == 0) {
@@ -1037,9 +1038,18 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
 // Each wave folds every fourth split with an online max (one pass over the
 // partials, loads unrolled), then the four wave states combine in LDS. It runs
 // as its own launch, so the partials are visible without any in-kernel fence.
-__global__ __launch_bounds__(kBlock) void attention_merge(const float* __restrict__ part,
-                                                          const float* __restrict__ ml, int splits,
-                                                          bf16_t* __restrict__ out) {
+struct MergeArgs {
+  const float* part;
+  const float* ml;
+  bf16_t* out;
+  long o_sb, o_sh, o_st;
+  int splits, Hq, Q;
+};
+
+__global__ __launch_bounds__(kBlock) void attention_merge(MergeArgs a) {
+  const float* __restrict__ part = a.part;
+  const float* __restrict__ ml = a.ml;
+  const int splits = a.splits;
   __shared__ float wm[4], wl[4];
   __shared__ float2 wacc[4][D / 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1093,8 +1103,10 @@ __global__ __launch_bounds__(kBlock) void attention_merge(const float* __restric
       sy = fmaf(f, wacc[w][lane].y, sy);
       lt = fmaf(f, wl[w], lt);
     }
-    out[orow * D + 2 * lane] = static_cast<bf16_t>(f2bf(sx / lt));
-    out[orow * D + 2 * lane + 1] = static_cast<bf16_t>(f2bf(sy / lt));
+    const long t = orow % a.Q, bh = orow / a.Q, h = bh % a.Hq, b = bh / a.Hq;
+    bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st;
+    dst[2 * lane] = static_cast<bf16_t>(f2bf(sx / lt));
+    dst[2 * lane + 1] = static_cast<bf16_t>(f2bf(sy / lt));
   }
 }
 
@@ -1215,8 +1227,9 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   else if (rows <= 4) launch_partial<4>(fused, a, st);
   else launch_partial<8>(fused, a, st);
   if (a.splits == 1 || launch_status() != HTN_OK) return launch_status();
+  MergeArgs m{a.part, a.ml, a.out, a.o_sb, a.o_sh, a.o_st, a.splits, a.Hq, a.Q};
   hipLaunchKernelGGL(attention_merge, dim3(static_cast<long>(a.B) * a.Hq * a.Q), dim3(kBlock), 0,
-                     st, a.part, a.ml, a.splits, a.out);
+                     st, m);
   return launch_status();
 }
 
@@ -1268,10 +1281,12 @@ extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, co
 
 extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                                      const void* keys, const void* values, int64_t cap,
-                                     const int64_t* positions, void* out, int64_t B, int64_t Hq,
+                                     const int64_t* positions, void* out, int64_t o_sb,
+                                     int64_t o_sh, int64_t o_st, int64_t B, int64_t Hq,
                                      int64_t Hkv, int64_t Q, void* scratch,
                                      htn_stream_t stream) {
   if (!q || !keys || !values || !positions || !out) return HTN_EINVAL;
+  if (o_sb < 0 || o_sh < 0 || o_st < 0) return HTN_EINVAL;
   if (Hkv <= 0 || Hq % Hkv != 0 || Q <= 0) return HTN_EINVAL;
   if (!aligned16(keys) || !aligned16(values)) return HTN_EUNSUPPORTED;
   // Query rows are read as bf16 pairs.
@@ -1281,6 +1296,7 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
   a.keys = static_cast<bf16_t*>(const_cast<void*>(keys));
   a.values = static_cast<bf16_t*>(const_cast<void*>(values));
   a.cap = cap; a.pos = positions; a.out = static_cast<bf16_t*>(out);
+  a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
   a.B = static_cast<int>(B); a.Hq = static_cast<int>(Hq); a.Hkv = static_cast<int>(Hkv);
   a.G = static_cast<int>(Hq / Hkv); a.Q = static_cast<int>(Q);
   return run_attention(false, a, scratch, static_cast<hipStream_t>(stream));
@@ -1312,5 +1328,6 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
   a.cap = cap; a.pos = positions; a.out = static_cast<bf16_t*>(out);
   a.B = static_cast<int>(B); a.Hkv = static_cast<int>(Hkv); a.G = static_cast<int>(groups);
   a.Hq = static_cast<int>(Hkv * groups); a.Q = 1;
+  a.o_sh = D; a.o_st = D; a.o_sb = static_cast<long>(a.Hq) * D;  // out [B, Hq, 128]
   return run_attention(true, a, scratch, static_cast<hipStream_t>(stream));
 }

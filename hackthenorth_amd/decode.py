@@ -139,13 +139,16 @@ def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=Non
 
 def _attention_chunks(q, keys, values, positions, groups):
     """grouped_attention over the T queries in chunks the kernel takes at once
-    (at most 8 queries and 32 query rows per kv head)."""
-    t = q.shape[2]
+    (at most 8 queries and 32 query rows per kv head), written token-major:
+    returns [B * T, Hq * 128] rows for the output projection, no transpose."""
+    b, heads, t, dim = q.shape
+    out = torch.empty((b, t, heads, dim), dtype=q.dtype, device=q.device)
     step = max(1, min(8, 32 // groups))
-    if t <= step:
-        return grouped_attention(q, keys, values, positions)
-    return torch.cat([grouped_attention(q[:, :, s:s + step], keys, values, positions[s:s + step])
-                      for s in range(0, t, step)], dim=2)
+    for s in range(0, t, step):
+        e = min(t, s + step)
+        grouped_attention(q[:, :, s:e], keys, values, positions[s:e],
+                          out=out[:, s:e].transpose(1, 2))
+    return out.view(b * t, heads * dim)
 
 
 def _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings, rotary):
@@ -176,7 +179,6 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                                   layer.k_norm, cos, sin, cache.keys[i], cache.values[i],
                                   positions)
         a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
-        a = a.transpose(1, 2).reshape(rows, -1).contiguous()
         if multi:
             r = residual_rows(a, layer.o_weight, h)
             m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)

@@ -24,8 +24,11 @@ def _check_cache(keys, values, batch, kv_heads):
         raise ValueError("caches must be contiguous bf16 [B, Hkv, capacity, 128]")
 
 
-def grouped_attention(q, k, v, positions):
-    """softmax(q k^T / sqrt(128)) v per query over its visible slots (attention.py:213-237)."""
+def grouped_attention(q, k, v, positions, out=None):
+    """softmax(q k^T / sqrt(128)) v per query over its visible slots (attention.py:213-237).
+
+    `out`, when given, is a bf16 [B, Hq, Q, 128] view with unit dim stride
+    (for example a transposed token-major buffer) that receives the rows."""
     batch, heads, queries, dim = q.shape
     kv_heads = k.shape[1]
     if dim != _lib.HEAD_DIM or q.stride(-1) != 1 or q.dtype != torch.bfloat16:
@@ -35,13 +38,16 @@ def grouped_attention(q, k, v, positions):
     _check_cache(k, v, batch, kv_heads)
     if positions.dtype != torch.int64 or positions.numel() != queries:
         raise ValueError("positions must be int64 with one entry per query")
-    _lib.require_gpu(q, k, v, positions)
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must be a bf16 view shaped like q with unit dim stride")
+    _lib.require_gpu(q, k, v, positions, out)
     scratch = _scratch(q.device, batch, heads, queries, k.shape[2])
     _lib.call("htn_grouped_attention", _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2),
               _lib.ptr(k), _lib.ptr(v), k.shape[2], _lib.ptr(positions.contiguous()),
-              _lib.ptr(out), batch, heads, kv_heads, queries, _lib.ptr(scratch),
-              _lib.stream(q.device))
+              _lib.ptr(out), out.stride(0), out.stride(1), out.stride(2), batch, heads,
+              kv_heads, queries, _lib.ptr(scratch), _lib.stream(q.device))
     return out
 
 

@@ -218,15 +218,18 @@ int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t ca
 /* Grouped-query attention over fixed-capacity caches with causality by
  * absolute position: query t of head h sees slots <= positions[t] of kv head
  * h / (Hq / Hkv); later slots are never read. q[b, h, t, :] at
- * q + b*q_sb + h*q_sh + t*q_st; out is [B, Hq, Q, 128] contiguous.
+ * q + b*q_sb + h*q_sh + t*q_st; out[b, h, t, :] at out + b*o_sb + h*o_sh +
+ * t*o_st (element strides; dims contiguous), so a token-major [B, Q, Hq, 128]
+ * output feeds the output projection without a transpose.
  * Split-KV: one launch writes per-split partials to `scratch`
  * (htn_attention_scratch_bytes), a second merges them (one launch when the
  * context fits one split).
  * Replaces grouped_attention(q, k, v, positions), kernels/attention.py:213. */
 int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                           const void* keys, const void* values, int64_t cap,
-                          const int64_t* positions, void* out, int64_t B, int64_t Hq,
-                          int64_t Hkv, int64_t Q, void* scratch, htn_stream_t stream);
+                          const int64_t* positions, void* out, int64_t o_sb, int64_t o_sh,
+                          int64_t o_st, int64_t B, int64_t Hq, int64_t Hkv, int64_t Q,
+                          void* scratch, htn_stream_t stream);
 
 /* Single-token decode attention with the QK-norm/RoPE/cache append fused in:
  * q, the newest k and v come from the packed projection row
