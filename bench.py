@@ -332,21 +332,25 @@ def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
             "affinity_cpus": len(os.sched_getaffinity(0))}
 
 
-def pmc_pass():
+def pmc_pass(shape="qwen3-0.6b"):
     """Short, graph-free workload for rocprofv3 --pmc passes (counter collection
     is per dispatch, so every kernel is launched eagerly): 8 decode steps of the
-    0.6B workload at context 512, 28 launches of the dominant kernel over the
-    layers' weights, and a 256 MiB device copy (reads and writes exactly 256 MiB)
-    that calibrates the byte counters."""
-    cfg = shape_config("qwen3-0.6b")
+    shape's workload (0.6B at context 512, 8B at context 2048 over a synthetic
+    cache), one launch of the dominant kernel per layer over the layers'
+    weights, and a 256 MiB device copy (reads and writes exactly 256 MiB) that
+    calibrates the byte counters."""
+    cfg = shape_config(shape)
     model = Qwen3Model.random(cfg)
-    cap = 512 + 8
+    ctx = 512 if shape == "qwen3-0.6b" else 2048
+    cap = ctx + 8
     with torch.inference_mode():
         cache = D.KVCache(model, 1, cap)
+        if ctx > 512:
+            DR.normal_(cache.storage.view(-1), 21, 77, 1.0)
         rotary = D.RotaryTable(model, cap)
         token = torch.zeros((1, 1), dtype=torch.int64, device=model.device)
         for i in range(8):
-            pos = torch.tensor([512 + i], dtype=torch.int64, device=model.device)
+            pos = torch.tensor([ctx + i], dtype=torch.int64, device=model.device)
             token = D.forward(model, token, cache, pos, rotary=rotary)
         x = torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16, device=model.device)
         DR.normal_(x, 3, 99, 1.0)
@@ -374,6 +378,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-8b", action="store_true")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--pmc-shape", default="qwen3-0.6b", choices=("qwen3-0.6b", "qwen3-8b"),
+                    help="model shape of the --pmc-pass workload")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
@@ -390,7 +396,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_pass:
-        pmc_pass()
+        pmc_pass(args.pmc_shape)
         return
 
     def log(msg):
