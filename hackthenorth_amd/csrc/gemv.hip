@@ -469,13 +469,14 @@ constexpr long kWavesPerCu = 16;
 template <int R, int S, int U, bool NORM, int EPI, int WF>
 int launch_vec(const GemvArgs& a, hipStream_t st) {
   const long groups = (a.n + R - 1) / R;
-  // RMSNorm kernels pay their prologue once per block: when every wave would
-  // stream three or more row groups anyway, two longer-lived blocks per CU
-  // beat four. Kernels without a prologue fill the CU.
+  // RMSNorm kernels pay their prologue once per block: two longer-lived
+  // blocks per CU beat four (measured from 3072 to 151936 row groups: e.g. the
+  // 6144-row, K = 4096 QKV projection takes 9.9 us at two, 10.6 us at four).
+  // Kernels without a prologue fill the CU.
   // 8-bit rows are half as long, so a wave holds half the bytes in flight:
   // their norm kernels keep four blocks per CU (eight for 1 KB rows).
   long per_cu = 8;
-  if (NORM && WF == WF_BF16) per_cu = groups >= 3 * kWavesPerCu * device_cus() ? 2 : 4;
+  if (NORM && WF == WF_BF16) per_cu = 2;
   if (NORM && WF != WF_BF16) per_cu = a.k > 1024 ? 4 : 8;
   const long blocks = grid_for(groups, per_cu);
   const size_t lds = NORM ? static_cast<size_t>(a.k) * 2 : 0;
