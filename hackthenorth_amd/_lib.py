@@ -58,6 +58,8 @@ SIGNATURES = {
                               _I64, _I64, _I64, _I64, _P, _P],
     "htn_prologue_attention": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64, _I,
                                _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P],
+    "htn_xcc_ids": [_P, _I64, _P],
+    "htn_attention_merge_in_kernel": [],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64}
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3

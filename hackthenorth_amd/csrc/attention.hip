@@ -7,16 +7,22 @@
 //    query rows of its kv head once, streams its slice of K then V with
 //    16-byte loads (16 lanes per 256-byte cache row, four rows per wave
 //    instruction), keeps scores in LDS for an exact two-pass softmax, and
-//    writes an unnormalised partial plus (max, sum); a second launch merges
-//    the partials per output row (log-sum-exp weights). A block never waits
-//    for other blocks: an agent-scope release per block (L2 write-back on
-//    gfx950) costs far more than the extra launch.
+//    writes an unnormalised partial plus (max, sum), merged per output row
+//    with log-sum-exp weights. Workgroups are dispatched to the XCDs
+//    round-robin, so the grid is laid out XCD-affine: every split of one
+//    (batch, kv head) pair runs on the same XCD, and the last of them to
+//    finish merges the pair's rows out of that XCD's L2 (the partials never
+//    need to be visible to other XCDs, so no agent-scope release, which is an
+//    L2 write-back on gfx950, is ever issued). Without that layout a second
+//    launch merges the partials.
 //  * slots after a query's absolute position are masked; slots after the
 //    largest position are never read.
 //  * the fused prologue variant computes q and the newest k/v from the packed
 //    projection row, appends k/v to the cache, and feeds the newest slot from
 //    LDS so the appended row is never re-read from memory.
 #include "common.h"
+
+#include <stdlib.h>
 
 namespace htn {
 
@@ -26,6 +32,12 @@ constexpr int kSplit = 64;          // cache slots per tile
 constexpr int kMinSplit = 16;       // fewest slots a block is given
 constexpr int kMaxQ = 8;            // queries per launch (verify rows)
 constexpr int kMergeUnroll = 16;    // partials loaded back to back in the merge
+// Arrival counters of the in-kernel merge, at the head of the scratch buffer:
+// one 128-byte line per (batch, kv head) pair.
+constexpr int kCounterStride = 32;  // uint32 words
+constexpr int kMaxCounterPairs = 256;
+constexpr long kCounterBytes = static_cast<long>(kMaxCounterPairs) * kCounterStride * 4;
+static_assert(kCounterBytes == HTN_ATTENTION_COUNTER_BYTES, "counter region size");
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
 //   n = bf16(g * bf16(x * inv)); out_i = bf16(bf16(n_i cos_i) + bf16(rot(n)_i sin_i)).
@@ -173,7 +185,98 @@ struct AttnArgs {
   int B, Hq, Hkv, G, Q, splits, split, stream;
   int ring;             // LDS-staged kernel: tiles staged ahead (0: other kernels)
   float scale;
+  unsigned* done;       // arrival counters: XCD-affine grid, in-kernel merge (else null)
 };
+
+// Block coordinates (split s, kv head, batch). With the in-kernel merge the
+// grid is one-dimensional: block L runs on XCD L % 8 (round-robin dispatch;
+// on 1, 2 or 4 XCDs blocks with equal L % 8 still share one), and the splits
+// of pair p = b * Hkv + kvh take blocks L = ((p / 8) * splits + s) * 8 + p % 8.
+// Blocks past the last pair (pairs are padded to a multiple of 8) return false.
+__device__ __forceinline__ bool split_coords(const AttnArgs& a, int& s, int& kvh, int& b) {
+  if (!a.done) {
+    s = blockIdx.x;
+    kvh = blockIdx.y;
+    b = blockIdx.z;
+    return true;
+  }
+  // The divisions run on the vector unit: readfirstlane keeps the results
+  // (block-uniform) in scalar registers for the descriptors built from them.
+  const int L = blockIdx.x, j = L >> 3;
+  const int g = __builtin_amdgcn_readfirstlane(j / a.splits);
+  s = j - g * a.splits;
+  const int p = g * 8 + (L & 7);
+  b = __builtin_amdgcn_readfirstlane(p / a.Hkv);
+  kvh = p - b * a.Hkv;
+  return p < a.B * a.Hkv;
+}
+
+// Agent-scope (sc1) loads: they miss the CU's L1, so they observe what other
+// CUs of this XCD stored to its L2.
+__device__ __forceinline__ float2 load_f2_sc1(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 16);
+  return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+}
+
+// One output row of the in-kernel merge with every load in flight at once:
+// lane j holds split j's (max, sum); N >= S partials per lane (past S the
+// descriptor reads zeros, and those splits weigh 0).
+template <int N>
+__device__ __forceinline__ void merge_row_short(__amdgpu_buffer_rsrc_t prs, __amdgpu_buffer_rsrc_t mrs,
+                                                int S, int lane, float& num_x, float& num_y,
+                                                float& den) {
+  const float2 ml = load_f2_sc1(mrs, lane * 8);
+  float2 pv[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) pv[u] = load_f2_sc1(prs, (u * D + 2 * lane) * 4);
+  __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first wait
+  const float M = wave_max(lane < S ? ml.x : -INFINITY);
+  const float w = lane < S && ml.x != -INFINITY ? expf(ml.x - M) : 0.f;
+  den = wave_sum(w * ml.y);
+  num_x = num_y = 0.f;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float wu = readlane(w, u);
+    num_x = fmaf(wu, pv[u].x, num_x);
+    num_y = fmaf(wu, pv[u].y, num_y);
+  }
+}
+
+// End of a split block on the XCD-affine grid. Every thread's partial stores
+// have completed in the XCD's L2 before the block counts itself in; the block
+// that brings its pair's count to `splits` merges the pair's G * Q rows (one
+// wave per row) and rearms the counter for the next launch:
+//   out = sum_s w_s acc_s / sum_s w_s l_s,  w_s = exp(m_s - M),  M = max_s m_s.
+// Every load of a row is in flight at once (the host takes this path for at
+// most four rows of at most 48 splits).
+__device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, int* last) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int p = b * a.Hkv + kvh;
+  unsigned* cnt = a.done + static_cast<long>(p) * kCounterStride;
+  if (threadIdx.x == 0)
+    *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            static_cast<unsigned>(a.splits - 1);
+  __syncthreads();
+  if (!*last) return;
+  // A wave-uniform row index keeps the row's descriptors in scalar registers.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int R = a.G * a.Q, S = a.splits;
+  for (int r = wave; r < R; r += kBlock / kWave) {
+    const long orow = static_cast<long>(p) * R + r;
+    const __amdgpu_buffer_rsrc_t prs =
+        buffer_rsrc(a.part + orow * S * D, static_cast<uint32_t>(S) * D * 4);
+    const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(a.ml + orow * S * 2, static_cast<uint32_t>(S) * 8);
+    float nx, ny, den;
+    if (S <= 16) merge_row_short<16>(prs, mrs, S, lane, nx, ny, den);
+    else merge_row_short<48>(prs, mrs, S, lane, nx, ny, den);
+    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
+    bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st;
+    *reinterpret_cast<uint32_t*>(dst + 2 * lane) = pack_bf2(nx / den, ny / den);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Query source of the partial kernel: q rows from memory, or the fused
 // prologue over the packed projection row with the RoPE row either already
@@ -211,10 +314,12 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   __shared__ int rowpos[kMaxRows];  // absolute position of each query row
   __shared__ __align__(16) bf16_t knew[D];
   __shared__ __align__(16) bf16_t vnew[D];
+  __shared__ int last_split;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane >> 4, e = lane & 15;
-  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int s, kvh, b;
+  if (!split_coords(a, s, kvh, b)) return;
   const int rows = a.G * a.Q;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
   // The block owns slots [start, stop): a.split slots (at most SPLIT).
@@ -442,6 +547,7 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
     }
     __syncthreads();
   }
+  if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
 // Streaming split-KV attention for long contexts: a block owns T (even)
@@ -781,12 +887,14 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
   __shared__ float wacc[kBlock / kWave][ROWS][D];
   __shared__ __align__(16) bf16_t knew[D];
   __shared__ __align__(16) bf16_t vnew[D];
+  __shared__ int last_split;
 
   // The wave index is uniform: readfirstlane keeps LDS and tile offsets scalar.
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int sub = lane >> 4, e = lane & 15;
-  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int s, kvh, b;
+  if (!split_coords(a, s, kvh, b)) return;
   const int rows = a.G;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
   const int start = s * a.split;
@@ -1031,6 +1139,7 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
       }
     }
   }
+  if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
 // Merge of the split partials, one block per output row (b, h, t):
@@ -1116,9 +1225,17 @@ using namespace htn;
 
 namespace {
 
+// (split, kv head, batch), or the one-dimensional XCD-affine grid: eight
+// block columns, each holding the splits of every eighth pair.
+dim3 split_grid(const AttnArgs& a) {
+  if (!a.done) return dim3(a.splits, a.Hkv, a.B);
+  const long pairs = static_cast<long>(a.B) * a.Hkv;
+  return dim3(static_cast<unsigned>(8 * ((pairs + 7) / 8) * a.splits));
+}
+
 template <int ROWS, int TILES>
 void launch_partial_t(bool fused, const AttnArgs& a, hipStream_t st) {
-  const dim3 grid(a.splits, a.Hkv, a.B);
+  const dim3 grid = split_grid(a);
   if (!fused)
     hipLaunchKernelGGL((attention_partial<ROWS, PRO_NONE, TILES>), grid, dim3(kBlock), 0, st, a);
   else if (a.rope_by_pos)
@@ -1145,8 +1262,7 @@ void launch_lds_t(const AttnArgs& a, hipStream_t st) {
       reinterpret_cast<const void*>(&attention_lds<ROWS, PRO, RING>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   (void)attr;  // a refused size surfaces as a launch error
-  hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING>), dim3(a.splits, a.Hkv, a.B), dim3(kBlock),
-                     lds, st, a);
+  hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
 }
 
 template <int ROWS, int PRO>
@@ -1170,6 +1286,24 @@ void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
   }
   if (a.split > kSplit) launch_partial_t<ROWS, 2>(fused, a, st);
   else launch_partial_t<ROWS, 1>(fused, a, st);
+}
+
+// The in-kernel merge needs every block with equal index mod 8 on one XCD:
+// true for round-robin dispatch over 1, 2, 4 or 8 XCDs. Setting
+// HTN_ATTENTION_MERGE_LAUNCH=1 keeps the separate merge launch instead.
+bool xcd_affine_merge() {
+  static int state[64];  // per device: 0 unknown, 1 on, 2 off
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (state[dev] == 0) {
+    int n = 0;
+    const char* env = getenv("HTN_ATTENTION_MERGE_LAUNCH");
+    const bool ok = !(env && env[0] == '1') &&
+                    hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
+                    (n == 1 || n == 2 || n == 4 || n == 8);
+    state[dev] = ok ? 1 : 2;
+  }
+  return state[dev] == 1;
 }
 
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
@@ -1218,15 +1352,26 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   a.split = static_cast<int>(split);
   a.splits = static_cast<int>((a.cap + a.split - 1) / a.split);
   if (a.splits > 1 && !scratch) return HTN_EINVAL;
+  // Scratch: the arrival counters, then the partials and their (max, sum).
   const long nrow = static_cast<long>(a.B) * a.Hq * a.Q * a.splits;
-  a.part = static_cast<float*>(scratch);
+  unsigned char* sbase = static_cast<unsigned char*>(scratch);
+  a.part = sbase ? reinterpret_cast<float*>(sbase + kCounterBytes) : nullptr;
   a.ml = a.part ? a.part + nrow * D : nullptr;
+  a.done = nullptr;
+  // The in-kernel merge stores each lane's two output dims as one 32-bit word.
+  const bool out_pairs = !(reinterpret_cast<uintptr_t>(a.out) & 3u) && !((a.o_sb | a.o_sh | a.o_st) & 1);
+  // One block merges a pair's rows, each row's loads all in flight: worth it
+  // up to four rows (one per wave) of at most 48 splits. More rows or splits
+  // go to the merge launch, which spreads the rows over the GPU.
+  if (a.splits > 1 && a.splits <= 48 && rows <= 4 && !a.stream && heads <= kMaxCounterPairs &&
+      out_pairs && xcd_affine_merge())
+    a.done = reinterpret_cast<unsigned*>(sbase);
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
   if (rows <= 1) launch_partial<1>(fused, a, st);
   else if (rows <= 2) launch_partial<2>(fused, a, st);
   else if (rows <= 4) launch_partial<4>(fused, a, st);
   else launch_partial<8>(fused, a, st);
-  if (a.splits == 1 || launch_status() != HTN_OK) return launch_status();
+  if (a.splits == 1 || a.done || launch_status() != HTN_OK) return launch_status();
   MergeArgs m{a.part, a.ml, a.out, a.o_sb, a.o_sh, a.o_st, a.splits, a.Hq, a.Q};
   hipLaunchKernelGGL(attention_merge, dim3(static_cast<long>(a.B) * a.Hq * a.Q), dim3(kBlock), 0,
                      st, m);
@@ -1239,7 +1384,7 @@ extern "C" int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q,
   if (B <= 0 || Hq <= 0 || Q <= 0 || cap <= 0) return 0;
   // The smallest split the plan picks is kMinSplit slots.
   const long splits = (cap + kMinSplit - 1) / kMinSplit;
-  return static_cast<long>(B) * Hq * Q * splits * (D + 2) * 4;
+  return kCounterBytes + static_cast<long>(B) * Hq * Q * splits * (D + 2) * 4;
 }
 
 extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k,
@@ -1331,3 +1476,25 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
   a.o_sh = D; a.o_st = D; a.o_sb = static_cast<long>(a.Hq) * D;  // out [B, Hq, 128]
   return run_attention(true, a, scratch, static_cast<hipStream_t>(stream));
 }
+
+namespace htn {
+
+// Diagnostic: the XCD (hardware register XCC_ID) each block of a one-
+// dimensional grid runs on, for checking the round-robin dispatch that the
+// XCD-affine attention grid relies on.
+__global__ __launch_bounds__(kWave) void xcc_ids_kernel(int32_t* out, long n) {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  if (threadIdx.x == 0 && blockIdx.x < n) out[blockIdx.x] = static_cast<int32_t>(v & 0xfu);
+}
+
+}  // namespace htn
+
+extern "C" int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream) {
+  if (!out || blocks <= 0 || blocks > (1L << 20)) return HTN_EINVAL;
+  hipLaunchKernelGGL(xcc_ids_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
+                     static_cast<hipStream_t>(stream), out, static_cast<long>(blocks));
+  return launch_status();
+}
+
+extern "C" int htn_attention_merge_in_kernel() { return xcd_affine_merge() ? 1 : 0; }

@@ -11,9 +11,27 @@ import torch
 from .. import _lib
 
 
+# (device index, stream handle) -> zero-initialised scratch buffers, newest last.
+_SCRATCH = {}
+
+
 def _scratch(device, batch, heads, queries, capacity):
-    nbytes = _lib.load().htn_attention_scratch_bytes(batch, heads, queries, capacity)
-    return torch.empty((max(nbytes, 4) + 3) // 4, dtype=torch.float32, device=device)
+    """The attention scratch of the current stream. Its leading arrival
+    counters must be zero before a call and every call leaves them zero, so
+    one zero-filled buffer per stream is kept and reused (calls on one stream
+    are ordered; buffers of different streams never meet). It only grows, and
+    outgrown buffers are kept: a captured graph may still use their address.
+    During capture a too-small buffer is not replaced: the call gets a fresh
+    zero-filled one, whose fill the graph records ahead of the kernel."""
+    nbytes = max(_lib.load().htn_attention_scratch_bytes(batch, heads, queries, capacity), 4)
+    current = torch.cuda.current_stream(device)
+    buffers = _SCRATCH.setdefault((current.device_index, current.cuda_stream), [])
+    if buffers and buffers[-1].numel() * 4 >= nbytes:
+        return buffers[-1]
+    buffer = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
+    if not torch.cuda.is_current_stream_capturing():
+        buffers.append(buffer)
+    return buffer
 
 
 def _check_cache(keys, values, batch, kv_heads):

@@ -12,9 +12,12 @@
  *
  * "scratch" buffers are caller-owned device memory for per-block partial
  * results, sized as each entry point states; no initial contents are
- * required. Calls that run concurrently on one scratch buffer race.
- * No kernel synchronises across its own blocks: every cross-block reduction
- * is finished by a second, stream-ordered launch.
+ * required, except the attention scratch's leading arrival counters (see
+ * htn_attention_scratch_bytes). Calls that run concurrently on one scratch
+ * buffer race.
+ * Cross-block reductions are finished by a second, stream-ordered launch,
+ * except the split-KV attention merge, which the last split of each (batch,
+ * kv head) pair performs in the same launch (see htn_grouped_attention).
  *
  * Reference interfaces cited as file:line are in rickytang666/hackthenorth,
  * under dryft/engine/.
@@ -212,7 +215,11 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
                         const int64_t* positions, void* out_q, void* out_k, int64_t B,
                         int64_t T, int64_t Hq, int64_t Hkv, htn_stream_t stream);
 
-/* Bytes of fp32 scratch the attention entry points need for these sizes. */
+/* Bytes of scratch the attention entry points need for these sizes. The first
+ * HTN_ATTENTION_COUNTER_BYTES hold arrival counters: zero them once when the
+ * buffer is allocated; every call leaves them zero. Calls sharing a scratch
+ * buffer must be ordered (one stream). */
+#define HTN_ATTENTION_COUNTER_BYTES 32768
 int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap);
 
 /* Grouped-query attention over fixed-capacity caches with causality by
@@ -221,9 +228,14 @@ int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t ca
  * q + b*q_sb + h*q_sh + t*q_st; out[b, h, t, :] at out + b*o_sb + h*o_sh +
  * t*o_st (element strides; dims contiguous), so a token-major [B, Q, Hq, 128]
  * output feeds the output projection without a transpose.
- * Split-KV: one launch writes per-split partials to `scratch`
- * (htn_attention_scratch_bytes), a second merges them (one launch when the
- * context fits one split).
+ * Split-KV: each split writes an unnormalised partial and its (max, sum) to
+ * `scratch` (htn_attention_scratch_bytes). Workgroups are dispatched to the
+ * XCDs round-robin, so the splits of one (batch, kv head) pair are laid on a
+ * single XCD and the last of them to arrive merges the pair's rows from that
+ * XCD's L2 in the same launch. Where the device's XCD count does not divide
+ * 8, for more than 256 (batch, kv head) pairs, for the streaming long-context
+ * kernel, or with the environment variable HTN_ATTENTION_MERGE_LAUNCH=1, a
+ * second launch merges instead. One launch when the context fits one split.
  * Replaces grouped_attention(q, k, v, positions), kernels/attention.py:213. */
 int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                           const void* keys, const void* values, int64_t cap,
@@ -245,6 +257,15 @@ int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64
                            int64_t cap,
                            const int64_t* positions, void* out, int64_t B, int64_t Hkv,
                            int64_t groups, void* scratch, htn_stream_t stream);
+
+/* Diagnostics of the in-kernel attention merge; no counterpart in the
+ * reference. htn_xcc_ids writes, for each block b < blocks of a
+ * one-dimensional grid, the XCD it ran on (hardware register XCC_ID), so a
+ * test can confirm the round-robin dispatch the merge relies on (blocks with
+ * equal index mod 8 share an XCD). htn_attention_merge_in_kernel returns 1 if
+ * the attention entry points merge splits in-kernel on the current device. */
+int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream);
+int htn_attention_merge_in_kernel(void);
 
 #ifdef __cplusplus
 }

@@ -243,6 +243,49 @@ def test_decode_attention_group_sizes_match_oracle(heads, kv_heads, position, ca
     close(actual, expected)
 
 
+def test_xcd_dispatch_keeps_block_columns_on_one_xcd():
+    # The in-kernel split merge lays every split of a (batch, kv head) pair on
+    # blocks with equal index mod 8 and relies on the round-robin workgroup
+    # dispatch putting all of those on one XCD.
+    lib = _lib.load()
+    blocks = 4099
+    ids = torch.full((blocks,), -1, dtype=torch.int32, device="cuda")
+    assert lib.htn_xcc_ids(_lib.ptr(ids), blocks, _lib.stream()) == _lib.HTN_OK
+    ids = ids.cpu()
+    assert int(ids.min()) >= 0
+    assert torch.equal(ids, ids[torch.arange(blocks) % 8])
+    print("XCDs seen:", sorted(set(ids.tolist())), "in-kernel merge:",
+          lib.htn_attention_merge_in_kernel())
+
+
+@pytest.mark.parametrize("batch,heads,kv_heads,position,capacity",
+                         [(1, 4, 1, 700, 1000), (3, 8, 2, 300, 600), (3, 16, 4, 1500, 2100),
+                          (5, 8, 8, 90, 200), (2, 8, 8, 5000, 8200)])
+def test_decode_attention_pair_counts_match_oracle(batch, heads, kv_heads, position, capacity):
+    # (batch, kv head) pair counts below, between and above multiples of 8:
+    # the split grid pads pairs to eight block columns.
+    q = nrm(36, (batch, 1, heads, 128)).transpose(1, 2)
+    k, v = nrm(37, (batch, kv_heads, capacity, 128)), nrm(38, (batch, kv_heads, capacity, 128))
+    k[:, :, position + 1:] = float("nan")
+    v[:, :, position + 1:] = float("nan")
+    positions = torch.tensor([position])
+    actual = A.grouped_attention(cuda(q.contiguous()), cuda(k), cuda(v), cuda(positions))
+    close(actual, Q.attention(q, k, v, positions))
+
+
+def test_split_merge_counters_rearm_across_calls():
+    # One stream's scratch serves every call: large, small, then large again
+    # split counts must each leave the arrival counters at zero.
+    cases = [(2, 2047, 2304), (1, 40, 129), (3, 1500, 2100), (2, 2047, 2304)]
+    for i, (batch, position, capacity) in enumerate(cases):
+        q = nrm(70 + i, (batch, 1, 32, 128)).transpose(1, 2)
+        k, v = nrm(80 + i, (batch, 8, capacity, 128)), nrm(90 + i, (batch, 8, capacity, 128))
+        positions = torch.tensor([position])
+        for _ in range(3):
+            actual = A.grouped_attention(cuda(q.contiguous()), cuda(k), cuda(v), cuda(positions))
+            close(actual, Q.attention(q, k, v, positions))
+
+
 @pytest.mark.parametrize("capacity,positions", [(257, (0, 63, 64, 256)),
                                                 (2080, (0, 511, 512, 2049)),
                                                 (640, (0, 1, 639)),
