@@ -221,6 +221,11 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   const long stride = static_cast<long>(gridDim.x) * 4;
   long grp = static_cast<long>(blockIdx.x) * 4 + wave;
   const int kv8 = a.k >> 3;
+  // Every kernel argument in scalar registers before the first branch: one
+  // round of scalar loads instead of two.
+  asm volatile("" ::"s"(a.w), "s"(a.x), "s"(a.y), "s"(a.n), "s"(a.k));
+  if constexpr (NORM) asm volatile("" ::"s"(a.gain), "s"(a.eps));
+  if constexpr (EPI == EPI_RESIDUAL) asm volatile("" ::"s"(a.res));
 
   // RMSNorm operands first: vector loads complete in issue order, so loading
   // x and the gain ahead of the weights lets the prologue start as soon as
