@@ -184,6 +184,7 @@ struct AttnArgs {
   float* ml;            // [B, Hq, Q, splits, 2]
   int B, Hq, Hkv, G, Q, splits, split, stream;
   int ring;             // LDS-staged kernel: tiles staged ahead (0: other kernels)
+  int mfma;             // LDS-staged kernel: tiles on the matrix cores
   float scale;
   unsigned* done;       // arrival counters: XCD-affine grid, in-kernel merge (else null)
 };
@@ -1142,6 +1143,389 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
   if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
+// ------------------------------------------------------------------ matrix-core tiles
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four quads'
+// copies of one query row): gfx950's row-swap permutes, no LDS round trip.
+// permlane16_swap pairs row r with row r ^ 1 and permlane32_swap the wave's
+// halves; both results of each swap hold the two partners.
+__device__ __forceinline__ float quad_max(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// K (rotated rows, per-lane source offsets kvoff) then V (plain rows) of this
+// wave's 16 slots of one tile: eight 1 KB LDS-direct loads, as stage_tile.
+__device__ __forceinline__ void stage_tile_mf(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                              unsigned char* wave_lds, int lane,
+                                              const uint32_t (&kvoff)[4], uint32_t tile_off) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(wave_lds + u * 1024), 16, kvoff[u],
+                                             tile_off, 0, 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(wave_lds + 4096 + u * 1024), 16,
+                                             lane * 16, tile_off + u * 1024, 0, 0);
+}
+
+// Wait until at most WAIT vector-memory operations are outstanding, then read
+// this lane's score operand (four 16-byte K chunks) and its V^T operands:
+// element k of vt[j] is V[slot 4 * quad + k][dim 16 * j + col].
+template <int WAIT>
+__device__ __forceinline__ void read_tile_mf(const uint32_t (&kaddr)[4], uint32_t vaddr, uint32_t ro,
+                                             uint4 (&k)[4], uint2 (&vt)[8]) {
+  u32x4 k0, k1, k2, k3;
+  asm volatile(
+      "s_waitcnt vmcnt(%4)\n\t"
+      "ds_read_b128 %0, %5\n\t"
+      "ds_read_b128 %1, %6\n\t"
+      "ds_read_b128 %2, %7\n\t"
+      "ds_read_b128 %3, %8"
+      : "=&v"(k0), "=&v"(k1), "=&v"(k2), "=&v"(k3)
+      : "n"(WAIT), "v"(kaddr[0] + ro), "v"(kaddr[1] + ro), "v"(kaddr[2] + ro), "v"(kaddr[3] + ro)
+      : "memory");
+  // Each 16-bit element in its own register (zero-extended), packed after
+  // the reads: no instruction merges into a register another read still
+  // has in flight.
+  uint32_t w[32];
+  const uint32_t va = vaddr + ro;
+  asm volatile(
+      "ds_read_u16 %0, %32 offset:0\n\t"
+      "ds_read_u16 %1, %32 offset:256\n\t"
+      "ds_read_u16 %2, %32 offset:512\n\t"
+      "ds_read_u16 %3, %32 offset:768\n\t"
+      "ds_read_u16 %4, %32 offset:32\n\t"
+      "ds_read_u16 %5, %32 offset:288\n\t"
+      "ds_read_u16 %6, %32 offset:544\n\t"
+      "ds_read_u16 %7, %32 offset:800\n\t"
+      "ds_read_u16 %8, %32 offset:64\n\t"
+      "ds_read_u16 %9, %32 offset:320\n\t"
+      "ds_read_u16 %10, %32 offset:576\n\t"
+      "ds_read_u16 %11, %32 offset:832\n\t"
+      "ds_read_u16 %12, %32 offset:96\n\t"
+      "ds_read_u16 %13, %32 offset:352\n\t"
+      "ds_read_u16 %14, %32 offset:608\n\t"
+      "ds_read_u16 %15, %32 offset:864\n\t"
+      "ds_read_u16 %16, %32 offset:128\n\t"
+      "ds_read_u16 %17, %32 offset:384\n\t"
+      "ds_read_u16 %18, %32 offset:640\n\t"
+      "ds_read_u16 %19, %32 offset:896\n\t"
+      "ds_read_u16 %20, %32 offset:160\n\t"
+      "ds_read_u16 %21, %32 offset:416\n\t"
+      "ds_read_u16 %22, %32 offset:672\n\t"
+      "ds_read_u16 %23, %32 offset:928\n\t"
+      "ds_read_u16 %24, %32 offset:192\n\t"
+      "ds_read_u16 %25, %32 offset:448\n\t"
+      "ds_read_u16 %26, %32 offset:704\n\t"
+      "ds_read_u16 %27, %32 offset:960\n\t"
+      "ds_read_u16 %28, %32 offset:224\n\t"
+      "ds_read_u16 %29, %32 offset:480\n\t"
+      "ds_read_u16 %30, %32 offset:736\n\t"
+      "ds_read_u16 %31, %32 offset:992\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+        "=&v"(w[6]), "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]),
+        "=&v"(w[12]), "=&v"(w[13]), "=&v"(w[14]), "=&v"(w[15]), "=&v"(w[16]), "=&v"(w[17]),
+        "=&v"(w[18]), "=&v"(w[19]), "=&v"(w[20]), "=&v"(w[21]), "=&v"(w[22]), "=&v"(w[23]),
+        "=&v"(w[24]), "=&v"(w[25]), "=&v"(w[26]), "=&v"(w[27]), "=&v"(w[28]), "=&v"(w[29]),
+        "=&v"(w[30]), "=&v"(w[31])
+      : "v"(va)
+      : "memory");
+  k[0] = make_uint4(k0.x, k0.y, k0.z, k0.w);
+  k[1] = make_uint4(k1.x, k1.y, k1.z, k1.w);
+  k[2] = make_uint4(k2.x, k2.y, k2.z, k2.w);
+  k[3] = make_uint4(k3.x, k3.y, k3.z, k3.w);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    vt[j] = make_uint2(w[4 * j] | (w[4 * j + 1] << 16), w[4 * j + 2] | (w[4 * j + 3] << 16));
+}
+
+template <int ROWS, int PRO, int RING>
+__global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
+  constexpr bool FUSED = PRO != PRO_NONE;
+  extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  __shared__ uint32_t qs[ROWS * D / 2];
+  __shared__ float wm[kBlock / kWave][ROWS], wl[kBlock / kWave][ROWS];
+  __shared__ float wacc[kBlock / kWave][ROWS][D];
+  __shared__ __align__(16) bf16_t knew[D];
+  __shared__ __align__(16) bf16_t vnew[D];
+  __shared__ int last_split;
+
+  // The wave index is uniform: readfirstlane keeps LDS and tile offsets scalar.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane >> 4, e = lane & 15;
+  int s, kvh, b;
+  if (!split_coords(a, s, kvh, b)) return;
+  const int rows = a.G;
+  const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
+  const int start = s * a.split;
+  const int stop = start + a.split < a.cap ? start + a.split : static_cast<int>(a.cap);
+  const int nt = (a.split + kSplit - 1) / kSplit;
+
+  // ---- 1. loads that gate the query rows (as in attention_partial), the
+  // newest v row, then the position.
+  const int head_slot = wave * 4 + sub;
+  const bool is_k = head_slot == a.G;
+  const bf16_t* qrow = a.qkv + static_cast<long>(b) * a.qkv_sb;
+  const bf16_t* hsrc = is_k ? qrow + a.k_off + static_cast<long>(kvh) * D
+                            : qrow + (static_cast<long>(kvh) * a.G +
+                                      (head_slot < a.G ? head_slot : 0)) * D;
+  Head16 hq;
+  uint2 va = make_uint2(0, 0), vb = make_uint2(0, 0);
+  if (PRO == PRO_ROW) head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos, a.sin, e, hq);
+  if (FUSED) {
+    const bf16_t* vsrc = qrow + a.v_off + static_cast<long>(kvh) * D;
+    va = *reinterpret_cast<const uint2*>(vsrc + 4 * e);
+    vb = *reinterpret_cast<const uint2*>(vsrc + 64 + 4 * e);
+  }
+  constexpr int kQL = (ROWS * (D / 2) + kBlock - 1) / kBlock;  // q pairs per thread
+  uint32_t qv[kQL];
+  if (!FUSED) {
+#pragma unroll
+    for (int j = 0; j < kQL; ++j) {
+      const int idx = tid + j * kBlock;
+      const int c = idx < rows * (D / 2) ? idx : 0;
+      const int h = kvh * a.G + c / (D / 2), d = 2 * (c % (D / 2));
+      qv[j] = *reinterpret_cast<const uint32_t*>(a.q + static_cast<long>(b) * a.q_sb +
+                                                 static_cast<long>(h) * a.q_sh + d);
+    }
+  }
+  // ---- 2. stage the first RING tiles at once, through descriptors over the
+  // block's slots up to the capacity (slots past the newest position are
+  // masked below); later tiles use descriptors over the visible slots only,
+  // which read as zeros past them without touching memory.
+  const uint32_t cap_range = static_cast<uint32_t>(stop - start) * D * 2;
+  const bf16_t* kb = a.keys + kv_base + static_cast<long>(start) * D;
+  const bf16_t* vb0 = a.values + kv_base + static_cast<long>(start) * D;
+  unsigned char* wave_ring = ring + wave * kLdsWaveTile;
+  const uint32_t wave_off = static_cast<uint32_t>(wave) * 16 * D * 2;  // this wave's 16 slots
+  // K rows are staged rotated: chunk c of slot s sits at column (c + s) % 16
+  // of the slot's 256-byte row, so the score operand's 16 slots (one column
+  // each) fall in 16 different bank groups.
+  uint32_t kvoff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int sl = 4 * u + (lane >> 4);
+    kvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - sl) & 15) * 16);
+  }
+  {
+    const __amdgpu_buffer_rsrc_t krs0 = buffer_rsrc(kb, cap_range);
+    const __amdgpu_buffer_rsrc_t vrs0 = buffer_rsrc(vb0, cap_range);
+#pragma unroll
+    for (int t = 0; t < RING; ++t)
+      stage_tile_mf(krs0, vrs0, wave_ring + t * kLdsTile, lane, kvoff,
+                    t * kSplit * D * 2 + wave_off);
+  }
+  const int64_t pv = a.pos[0];
+  const int pos = pv < 0 ? -1 : (pv >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(pv));
+  const int last = pos < a.cap ? pos : static_cast<int>(a.cap) - 1;
+  const int end = stop < last + 1 ? stop : last + 1;  // slots [start, end) are visible
+  const int newest = FUSED && pos >= 0 && pos < a.cap ? pos : -1;
+  const bool has_newest = newest >= start && newest < end;
+  if (PRO == PRO_BY_POSITION) {
+    const long ri = (newest >= 0 && newest < a.rope_rows) ? newest : 0;
+    head16_load(hsrc, pick_gain(a.qg, a.kg, is_k), a.cos + ri * a.rope_st,
+                a.sin + ri * a.rope_st, e, hq);
+  }
+
+  const uint32_t range = end > start ? static_cast<uint32_t>(end - start) * D * 2 : 0u;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kb, range);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vb0, range);
+
+  // ---- 3. query rows (and, fused, the newest k/v) into LDS
+  if (FUSED) {
+    const bool do_head = head_slot < a.G || (is_k && has_newest);
+    uint2 oa, ob;
+    head16_math(hq, is_k ? sgpr_f32(a.k_eps) : sgpr_f32(a.q_eps), oa, ob);
+    if (do_head && !is_k) {
+      qs[head_slot * (D / 2) + 2 * e] = oa.x;
+      qs[head_slot * (D / 2) + 2 * e + 1] = oa.y;
+      qs[head_slot * (D / 2) + 32 + 2 * e] = ob.x;
+      qs[head_slot * (D / 2) + 32 + 2 * e + 1] = ob.y;
+    } else if (do_head) {
+      const long slot = kv_base + static_cast<long>(newest) * D;
+      *reinterpret_cast<uint2*>(knew + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(knew + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(vnew + 4 * e) = va;
+      *reinterpret_cast<uint2*>(vnew + 64 + 4 * e) = vb;
+      *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = va;
+      *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kQL; ++j)
+      if (tid + j * kBlock < rows * (D / 2)) qs[tid + j * kBlock] = qv[j];
+  }
+  lds_barrier();
+  // ---- 4. tiles on the matrix cores. Per wave and tile (its 16 slots):
+  //   S^T = K Q^T   v_mfma_f32_16x16x32_bf16 x 4: slots are the M index,
+  //                 query rows (padded to 16) the N index, 32 dims per step;
+  //   O^T += V^T P^T  v_mfma_f32_16x16x16_bf16 x 8: 16 dims per step, K = the
+  //                 16 slots. The scores' D layout (lane: row = slot
+  //                 4 * quad + i, column = query row) is exactly the P^T
+  //                 operand layout, so P never leaves the registers.
+  // P is rounded to bf16 for the product (as the reference's kernel does);
+  // the denominator sums the fp32 weights. Online softmax in base 2.
+  const int col = lane & 15, quad = lane >> 4;
+  uint4 qb[4];  // B operand of the scores: query row col, 16-byte chunk 4 * quad + j
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    qb[j] = col < rows ? *reinterpret_cast<const uint4*>(qs + col * (D / 2) + (4 * quad + j) * 4)
+                       : make_uint4(0, 0, 0, 0);
+  const float scale2 = a.scale * 1.4426950408889634f;  // log2(e) / sqrt(D)
+  f32x4_t acc_o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc_o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_r = -INFINITY, l_r = 0.f;  // query row col (the same in all four quads)
+  const uint32_t wave_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(wave_ring)));
+  uint32_t kaddr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    kaddr[j] = wave_base + static_cast<uint32_t>(col * 256 + ((4 * quad + j + col) & 15) * 16);
+  const uint32_t vaddr = wave_base + 4096 + static_cast<uint32_t>(quad * 1024 + col * 2);
+
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    const int q = t % RING;
+    const uint32_t ro = static_cast<uint32_t>(q * kLdsTile);
+    const int later = nt - 1 - t < RING - 1 ? nt - 1 - t : RING - 1;  // tiles staged after t
+    uint4 kreg[4];
+    uint2 vt[8];
+    if (RING == 1 || later == 0) read_tile_mf<0>(kaddr, vaddr, ro, kreg, vt);
+    else if (RING == 2 || later == 1) read_tile_mf<8>(kaddr, vaddr, ro, kreg, vt);
+    else if (later == 2) read_tile_mf<16>(kaddr, vaddr, ro, kreg, vt);
+    else read_tile_mf<24>(kaddr, vaddr, ro, kreg, vt);
+    const int tbase = start + t * kSplit + wave * 16;  // this wave's first slot
+    if (has_newest && newest >= tbase && newest < tbase + 16) {  // wave-uniform
+      // The staged copy of the newest slot predates this step's append.
+      const int sn = newest - tbase;
+      if (col == sn) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          kreg[j] = *reinterpret_cast<const uint4*>(knew + (4 * quad + j) * 8);
+      }
+      const int kn = sn - 4 * quad;  // element of this lane's V^T operand, if in 0..3
+      if (kn >= 0 && kn < 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t v = vnew[16 * j + col];
+          if (kn == 0) vt[j].x = (vt[j].x & 0xffff0000u) | v;
+          else if (kn == 1) vt[j].x = (vt[j].x & 0xffffu) | (v << 16);
+          else if (kn == 2) vt[j].y = (vt[j].y & 0xffff0000u) | v;
+          else vt[j].y = (vt[j].y & 0xffffu) | (v << 16);
+        }
+      }
+    }
+    const bool full = tbase + 16 <= end;  // wave-uniform
+    if (!full) {
+      // Slots past the visible ones: V rows to zero (the cache may hold
+      // anything there, NaN included; never NaN * 0), scores to -inf below.
+      const int sb = tbase + 4 * quad;
+      const uint32_t mx = (sb < end ? 0xffffu : 0u) | (sb + 1 < end ? 0xffff0000u : 0u);
+      const uint32_t my = (sb + 2 < end ? 0xffffu : 0u) | (sb + 3 < end ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        vt[j].x &= mx;
+        vt[j].y &= my;
+      }
+    }
+    // Two accumulation chains of two steps each (shorter dependency chain).
+    f32x4_t st0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, st1 = st0;
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) {
+      st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j]),
+                                                    __builtin_bit_cast(bf16x8_t, qb[j]), st0, 0, 0, 0);
+      st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j + 1]),
+                                                    __builtin_bit_cast(bf16x8_t, qb[j + 1]), st1, 0, 0, 0);
+    }
+    const f32x4_t st = st0 + st1;
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = st[i] * scale2;
+      if (!full) sc[i] = tbase + 4 * quad + i < end ? sc[i] : -INFINITY;
+    }
+    const float tmax = quad_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    if (tmax != -INFINITY) {  // wave-uniform: visibility depends on the slot only
+      const float m_new = fmaxf(m_r, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_r - m_new);  // 0 on the first tile
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
+      l_r = fmaf(l_r, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+      m_r = m_new;
+      const uint2 pb = make_uint2(pack_bf2(p[0], p[1]), pack_bf2(p[2], p[3]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc_o[j] *= alpha;
+        acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, vt[j]),
+                                                             __builtin_bit_cast(short4_t, pb),
+                                                             acc_o[j], 0, 0, 0);
+      }
+    }
+    const int tn = t + RING;
+    if (tn < nt)  // wave-uniform
+      stage_tile_mf(krs, vrs, wave_ring + q * kLdsTile, lane, kvoff,
+                    tn * kSplit * D * 2 + wave_off);
+  }
+  // Every staging load has landed before the block's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- 5. the wave's state per query row: the denominator summed over the
+  // four quads' slots; O^T is spread one (dim, row) pair per lane register.
+  l_r = quad_sum(l_r);
+  if (col < rows) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wacc[wave][col][16 * j + 4 * quad + i] = acc_o[j][i];
+    if (quad == 0) {
+      wm[wave][col] = m_r;
+      wl[wave][col] = l_r;
+    }
+  }
+  lds_barrier();
+  for (int i = tid; i < rows * D; i += kBlock) {
+    const int r = i / D, d = i % D;
+    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+      const float f = wm[w][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][r] - M);
+      num = fmaf(f, wacc[w][r][d], num);
+      den = fmaf(f, wl[w][r], den);
+    }
+    const long orow = static_cast<long>(b) * a.Hq + kvh * a.G + r;
+    if (a.splits == 1) {
+      a.out[b * a.o_sb + (kvh * a.G + r) * a.o_sh + d] = static_cast<bf16_t>(f2bf(num / den));
+    } else {
+      a.part[(orow * a.splits + s) * D + d] = num;
+      if (d == 0) {
+        // the merge weighs partials with natural exponentials: max back to base e
+        a.ml[(orow * a.splits + s) * 2] = M * 0.6931471805599453f;
+        a.ml[(orow * a.splits + s) * 2 + 1] = den;
+      }
+    }
+  }
+  if (a.done) merge_tail(a, b, kvh, &last_split);
+}
+
 // Merge of the split partials, one block per output row (b, h, t):
 //   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
 // Each wave folds every fourth split with an online max (one pass over the
@@ -1265,8 +1649,24 @@ void launch_lds_t(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
 }
 
+template <int ROWS, int PRO, int RING>
+void launch_mfma_t(const AttnArgs& a, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(RING) * kLdsTile;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&attention_mfma<ROWS, PRO, RING>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  (void)attr;  // a refused size surfaces as a launch error
+  hipLaunchKernelGGL((attention_mfma<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
+}
+
 template <int ROWS, int PRO>
 void launch_lds_p(const AttnArgs& a, hipStream_t st) {
+  if (a.mfma) {
+    if (a.ring == 1) launch_mfma_t<ROWS, PRO, 1>(a, st);
+    else if (a.ring == 2) launch_mfma_t<ROWS, PRO, 2>(a, st);
+    else launch_mfma_t<ROWS, PRO, 4>(a, st);
+    return;
+  }
   if (a.ring == 1) launch_lds_t<ROWS, PRO, 1>(a, st);
   else if (a.ring == 2) launch_lds_t<ROWS, PRO, 2>(a, st);
   else launch_lds_t<ROWS, PRO, 4>(a, st);
@@ -1331,7 +1731,19 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
   long split = kSplit;
   a.stream = 0;
   a.ring = 0;
-  if (a.Q == 1 && rows <= 8 && (heads * tiles <= cus || heads * tiles > 2 * cus)) {
+  a.mfma = 0;
+  if (a.Q == 1 && rows <= 8 && heads <= 8 && tiles <= 144) {
+    // Up to 8 (batch, kv head) pairs and 9K slots (measured, 2 and 4 query
+    // rows per kv head, 512 to 8192 slots): one tile per block up to 24
+    // tiles, then two, then three (fewer splits leave the in-kernel merge
+    // less to read; four or more need the 128 KB ring, one block per CU).
+    // Four or more query rows per kv head score and weigh on the matrix
+    // cores; two rows are faster on the vector unit.
+    const long nt = tiles <= 24 ? 1 : (tiles <= 40 ? 2 : 3);
+    a.ring = nt == 1 ? 1 : 2;
+    a.mfma = rows >= 3;
+    split = nt * kSplit;
+  } else if (a.Q == 1 && rows <= 8 && (heads * tiles <= cus || heads * tiles > 2 * cus)) {
     // LDS per block: 32 KB per staged tile plus up to 19 KB (8 rows) of
     // state; two-tile rings fit two blocks per CU for rows <= 4. Between one
     // and two single-tile blocks per CU the register kernel below was
