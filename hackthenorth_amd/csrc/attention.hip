@@ -1257,12 +1257,21 @@ template <int ROWS, int PRO, int RING>
 __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  // MQ: several queries per sequence (16 or 32 rows = heads x queries, each
+  // with its own position); otherwise one query, up to 8 heads per kv head.
+  constexpr bool MQ = ROWS > 8;
+  constexpr int NT = (ROWS + 15) / 16;  // 16-row tiles of query rows
   __shared__ uint32_t qs[ROWS * D / 2];
   __shared__ float wm[kBlock / kWave][ROWS], wl[kBlock / kWave][ROWS];
-  __shared__ float wacc[kBlock / kWave][ROWS][D];
   __shared__ __align__(16) bf16_t knew[D];
   __shared__ __align__(16) bf16_t vnew[D];
+  __shared__ int rowpos[MQ ? ROWS : 1];  // absolute position of each query row
   __shared__ int last_split;
+  // The waves' partial states: with several queries they reuse the staging
+  // ring once every tile is read (the launch sizes it for both).
+  __shared__ float wacc_s[MQ ? 1 : kBlock / kWave][MQ ? 1 : ROWS][D];
+  float (*wacc)[ROWS][D] = MQ ? reinterpret_cast<float (*)[ROWS][D]>(ring)
+                              : reinterpret_cast<float (*)[ROWS][D]>(&wacc_s[0][0][0]);
 
   // The wave index is uniform: readfirstlane keeps LDS and tile offsets scalar.
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1270,7 +1279,7 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   const int sub = lane >> 4, e = lane & 15;
   int s, kvh, b;
   if (!split_coords(a, s, kvh, b)) return;
-  const int rows = a.G;
+  const int rows = a.G * a.Q;
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
   const int start = s * a.split;
   const int stop = start + a.split < a.cap ? start + a.split : static_cast<int>(a.cap);
@@ -1294,15 +1303,20 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   }
   constexpr int kQL = (ROWS * (D / 2) + kBlock - 1) / kBlock;  // q pairs per thread
   uint32_t qv[kQL];
+  int rpv = 0;
   if (!FUSED) {
 #pragma unroll
     for (int j = 0; j < kQL; ++j) {
       const int idx = tid + j * kBlock;
       const int c = idx < rows * (D / 2) ? idx : 0;
-      const int h = kvh * a.G + c / (D / 2), d = 2 * (c % (D / 2));
+      const int r = c / (D / 2), d = 2 * (c % (D / 2));
+      const int h = kvh * a.G + r / a.Q, t = r % a.Q;
       qv[j] = *reinterpret_cast<const uint32_t*>(a.q + static_cast<long>(b) * a.q_sb +
-                                                 static_cast<long>(h) * a.q_sh + d);
+                                                 static_cast<long>(h) * a.q_sh +
+                                                 static_cast<long>(t) * a.q_st + d);
     }
+    const int64_t v = a.pos[(tid < rows ? tid : 0) % a.Q];
+    rpv = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
   }
   // ---- 2. stage the first RING tiles at once, through descriptors over the
   // block's slots up to the capacity (slots past the newest position are
@@ -1330,10 +1344,24 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
       stage_tile_mf(krs0, vrs0, wave_ring + t * kLdsTile, lane, kvoff,
                     t * kSplit * D * 2 + wave_off);
   }
-  const int64_t pv = a.pos[0];
-  const int pos = pv < 0 ? -1 : (pv >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(pv));
-  const int last = pos < a.cap ? pos : static_cast<int>(a.cap) - 1;
-  const int end = stop < last + 1 ? stop : last + 1;  // slots [start, end) are visible
+  // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
+  int maxpos = -1, minpos = 1 << 30;
+  if (MQ) {
+    // Scalar loads of pos[min(t, Q - 1)] (in bounds, branch-free).
+#pragma unroll
+    for (int t = 0; t < kMaxQ; ++t) {
+      const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+      const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
+      maxpos = vc > maxpos ? vc : maxpos;
+      minpos = vc < minpos ? vc : minpos;
+    }
+  } else {
+    const int64_t v = a.pos[0];
+    minpos = maxpos = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
+  }
+  const int pos = minpos;  // one query: its position
+  const int last = maxpos < a.cap ? maxpos : static_cast<int>(a.cap) - 1;
+  const int end = stop < last + 1 ? stop : last + 1;  // slots [start, end) are visible to some row
   const int newest = FUSED && pos >= 0 && pos < a.cap ? pos : -1;
   const bool has_newest = newest >= start && newest < end;
   if (PRO == PRO_BY_POSITION) {
@@ -1368,6 +1396,7 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
       *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb;
     }
   } else {
+    if (MQ && tid < rows) rowpos[tid] = rpv;
 #pragma unroll
     for (int j = 0; j < kQL; ++j)
       if (tid + j * kBlock < rows * (D / 2)) qs[tid + j * kBlock] = qv[j];
@@ -1376,23 +1405,39 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   // ---- 4. tiles on the matrix cores. Per wave and tile (its 16 slots):
   //   S^T = K Q^T   v_mfma_f32_16x16x32_bf16 x 4: slots are the M index,
   //                 query rows (padded to 16) the N index, 32 dims per step;
-  //   O^T += V^T P^T  v_mfma_f32_16x16x16_bf16 x 8: 16 dims per step, K = the
-  //                 16 slots. The scores' D layout (lane: row = slot
+  //   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16 x 8: 16 dims per step, K = the
+  //                 16 slots, each once with the hi and once with the lo half
+  //                 of its weight. The scores' D layout (lane: row = slot
   //                 4 * quad + i, column = query row) is exactly the P^T
   //                 operand layout, so P never leaves the registers.
-  // P is rounded to bf16 for the product (as the reference's kernel does);
-  // the denominator sums the fp32 weights. Online softmax in base 2.
+  // P enters the product as two bf16 operands, hi = bf16(P) and
+  // lo = bf16(P - hi), so the weights keep about 16 bits (the VALU kernels
+  // multiply fp32 weights; a bf16-only P drifts from them by up to 2^-9
+  // relative per weight, enough to flip greedy near-ties between the
+  // one-query and the verify paths). The denominator sums the fp32 weights.
+  // Online softmax in base 2.
   const int col = lane & 15, quad = lane >> 4;
-  uint4 qb[4];  // B operand of the scores: query row col, 16-byte chunk 4 * quad + j
+  // Per 16-row tile n: B operand of the scores (query row col + 16 n, 16-byte
+  // chunk 4 * quad + j), the row's position, and its softmax state (the same
+  // in all four quads).
+  uint4 qb[NT][4];
+  int rp[NT];
+  f32x4_t acc_o[NT][8];
+  float m_r[NT], l_r[NT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    qb[j] = col < rows ? *reinterpret_cast<const uint4*>(qs + col * (D / 2) + (4 * quad + j) * 4)
-                       : make_uint4(0, 0, 0, 0);
+  for (int n = 0; n < NT; ++n) {
+    const int row = col + 16 * n;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      qb[n][j] = row < rows ? *reinterpret_cast<const uint4*>(qs + row * (D / 2) + (4 * quad + j) * 4)
+                            : make_uint4(0, 0, 0, 0);
+    rp[n] = MQ ? (row < rows ? rowpos[row] : -1) : pos;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc_o[n][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_r[n] = -INFINITY;
+    l_r[n] = 0.f;
+  }
   const float scale2 = a.scale * 1.4426950408889634f;  // log2(e) / sqrt(D)
-  f32x4_t acc_o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc_o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_r = -INFINITY, l_r = 0.f;  // query row col (the same in all four quads)
   const uint32_t wave_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(wave_ring)));
   uint32_t kaddr[4];
 #pragma unroll
@@ -1432,7 +1477,7 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
         }
       }
     }
-    const bool full = tbase + 16 <= end;  // wave-uniform
+    const bool full = tbase + 16 <= end;  // wave-uniform: every slot visible to some row
     if (!full) {
       // Slots past the visible ones: V rows to zero (the cache may hold
       // anything there, NaN included; never NaN * 0), scores to -inf below.
@@ -1445,38 +1490,52 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
         vt[j].y &= my;
       }
     }
-    // Two accumulation chains of two steps each (shorter dependency chain).
-    f32x4_t st0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, st1 = st0;
+    // Rows see slots up to their own position: masks are per lane, needed
+    // unless every row sees the wave's 16 slots.
+    const bool all_visible = tbase + 15 <= pos;  // wave-uniform (pos: the smallest position)
 #pragma unroll
-    for (int j = 0; j < 4; j += 2) {
-      st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j]),
-                                                    __builtin_bit_cast(bf16x8_t, qb[j]), st0, 0, 0, 0);
-      st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j + 1]),
-                                                    __builtin_bit_cast(bf16x8_t, qb[j + 1]), st1, 0, 0, 0);
-    }
-    const f32x4_t st = st0 + st1;
-    float sc[4];
+    for (int n = 0; n < NT; ++n) {
+      // Two accumulation chains of two steps each (shorter dependency chain).
+      f32x4_t st0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, st1 = st0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = st[i] * scale2;
-      if (!full) sc[i] = tbase + 4 * quad + i < end ? sc[i] : -INFINITY;
-    }
-    const float tmax = quad_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-    if (tmax != -INFINITY) {  // wave-uniform: visibility depends on the slot only
-      const float m_new = fmaxf(m_r, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m_r - m_new);  // 0 on the first tile
+      for (int j = 0; j < 4; j += 2) {
+        st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j]),
+                                                      __builtin_bit_cast(bf16x8_t, qb[n][j]), st0, 0, 0, 0);
+        st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kreg[j + 1]),
+                                                      __builtin_bit_cast(bf16x8_t, qb[n][j + 1]), st1, 0, 0, 0);
+      }
+      const f32x4_t st = st0 + st1;
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = st[i] * scale2;
+        if (!all_visible) sc[i] = tbase + 4 * quad + i <= rp[n] ? sc[i] : -INFINITY;
+      }
+      const float tmax = quad_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+      // One query: visibility depends on the slot only, so a wave whose 16
+      // slots are all hidden skips the tile (wave-uniform).
+      if (!MQ && tmax == -INFINITY) continue;
+      const float m_new = fmaxf(m_r[n], tmax);
+      // A row with nothing visible yet keeps weight 0 (no inf - inf).
+      const float ms = MQ && m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_r[n] - ms);  // 0 while m is -inf
       float p[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
-      l_r = fmaf(l_r, alpha, (p[0] + p[1]) + (p[2] + p[3]));
-      m_r = m_new;
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - ms);
+      l_r[n] = fmaf(l_r[n], alpha, (p[0] + p[1]) + (p[2] + p[3]));
+      m_r[n] = m_new;
       const uint2 pb = make_uint2(pack_bf2(p[0], p[1]), pack_bf2(p[2], p[3]));
+      const uint2 pl = make_uint2(pack_bf2(p[0] - bf_lo(pb.x), p[1] - bf_hi(pb.x)),
+                                  pack_bf2(p[2] - bf_lo(pb.y), p[3] - bf_hi(pb.y)));
+      // One K = 32 step per 16 dims: this lane's k values 0-3 pair its four
+      // V elements with hi, 4-7 the same V elements with lo.
+      const uint4 phl = make_uint4(pb.x, pb.y, pl.x, pl.y);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        acc_o[j] *= alpha;
-        acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, vt[j]),
-                                                             __builtin_bit_cast(short4_t, pb),
-                                                             acc_o[j], 0, 0, 0);
+        acc_o[n][j] *= alpha;
+        acc_o[n][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, make_uint4(vt[j].x, vt[j].y, vt[j].x, vt[j].y)),
+            __builtin_bit_cast(bf16x8_t, phl), acc_o[n][j], 0, 0, 0);
       }
     }
     const int tn = t + RING;
@@ -1489,15 +1548,22 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
 
   // ---- 5. the wave's state per query row: the denominator summed over the
   // four quads' slots; O^T is spread one (dim, row) pair per lane register.
-  l_r = quad_sum(l_r);
-  if (col < rows) {
+  // With several queries the states reuse the ring: every wave has finished
+  // reading it first.
+  if (MQ) lds_barrier();
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+  for (int n = 0; n < NT; ++n) {
+    const int row = col + 16 * n;
+    const float ln = quad_sum(l_r[n]);
+    if (row < rows) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wacc[wave][col][16 * j + 4 * quad + i] = acc_o[j][i];
-    if (quad == 0) {
-      wm[wave][col] = m_r;
-      wl[wave][col] = l_r;
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wacc[wave][row][16 * j + 4 * quad + i] = acc_o[n][j][i];
+      if (quad == 0) {
+        wm[wave][row] = m_r[n];
+        wl[wave][row] = ln;
+      }
     }
   }
   lds_barrier();
@@ -1511,9 +1577,10 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
       num = fmaf(f, wacc[w][r][d], num);
       den = fmaf(f, wl[w][r], den);
     }
-    const long orow = static_cast<long>(b) * a.Hq + kvh * a.G + r;
+    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
+    const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
     if (a.splits == 1) {
-      a.out[b * a.o_sb + (kvh * a.G + r) * a.o_sh + d] = static_cast<bf16_t>(f2bf(num / den));
+      a.out[b * a.o_sb + h * a.o_sh + t * a.o_st + d] = static_cast<bf16_t>(f2bf(num / den));
     } else {
       a.part[(orow * a.splits + s) * D + d] = num;
       if (d == 0) {
@@ -1651,12 +1718,28 @@ void launch_lds_t(const AttnArgs& a, hipStream_t st) {
 
 template <int ROWS, int PRO, int RING>
 void launch_mfma_t(const AttnArgs& a, hipStream_t st) {
-  const size_t lds = static_cast<size_t>(RING) * kLdsTile;
+  // The ring, which with several queries (ROWS > 8) the waves' partial states
+  // reuse after the last tile.
+  constexpr size_t kStates = ROWS > 8 ? static_cast<size_t>(kBlock / kWave) * ROWS * D * 4 : 0;
+  const size_t lds = static_cast<size_t>(RING) * kLdsTile > kStates ? static_cast<size_t>(RING) * kLdsTile
+                                                                     : kStates;
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&attention_mfma<ROWS, PRO, RING>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   (void)attr;  // a refused size surfaces as a launch error
   hipLaunchKernelGGL((attention_mfma<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
+}
+
+// Several queries per sequence (verify rows): 16 or 32 query rows per kv head.
+void launch_mfma_rows(const AttnArgs& a, hipStream_t st) {
+  const int rows = a.G * a.Q;
+  if (rows <= 16) {
+    if (a.ring == 1) launch_mfma_t<16, PRO_NONE, 1>(a, st);
+    else launch_mfma_t<16, PRO_NONE, 2>(a, st);
+  } else {
+    if (a.ring == 1) launch_mfma_t<32, PRO_NONE, 1>(a, st);
+    else launch_mfma_t<32, PRO_NONE, 2>(a, st);
+  }
 }
 
 template <int ROWS, int PRO>
@@ -1743,6 +1826,13 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
     a.ring = nt == 1 ? 1 : 2;
     a.mfma = rows >= 3;
     split = nt * kSplit;
+  } else if (!fused && a.Q > 1 && rows <= 32 && heads <= 8 && tiles <= 144) {
+    // Several queries (verify rows): the matrix-core kernel with per-row
+    // positions, 16 or 32 rows per block, the same split plan.
+    const long nt = tiles <= 24 ? 1 : (tiles <= 40 ? 2 : 3);
+    a.ring = nt == 1 ? 1 : 2;
+    a.mfma = 1;
+    split = nt * kSplit;
   } else if (a.Q == 1 && rows <= 8 && (heads * tiles <= cus || heads * tiles > 2 * cus)) {
     // LDS per block: 32 KB per staged tile plus up to 19 KB (8 rows) of
     // state; two-tile rings fit two blocks per CU for rows <= 4. Between one
@@ -1779,7 +1869,8 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
       out_pairs && xcd_affine_merge())
     a.done = reinterpret_cast<unsigned*>(sbase);
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
-  if (rows <= 1) launch_partial<1>(fused, a, st);
+  if (a.mfma && a.Q > 1) launch_mfma_rows(a, st);
+  else if (rows <= 1) launch_partial<1>(fused, a, st);
   else if (rows <= 2) launch_partial<2>(fused, a, st);
   else if (rows <= 4) launch_partial<4>(fused, a, st);
   else launch_partial<8>(fused, a, st);
