@@ -66,31 +66,74 @@ __device__ __forceinline__ void unpack4(uint2 v, float* o) {
   o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
 }
 
-// All 64 lanes must call this (16-lane DPP reduction).
-__device__ __forceinline__ void head16_math(const Head16& h, float eps, uint2& oa, uint2& ob) {
-  float xa[4], xb[4], ga[4], gb[4], ca[4], cb[4], sa[4], sb[4];
-  unpack4(h.xa, xa); unpack4(h.xb, xb); unpack4(h.ga, ga); unpack4(h.gb, gb);
-  unpack4(h.ca, ca); unpack4(h.cb, cb); unpack4(h.sa, sa); unpack4(h.sb, sb);
+// The head's sum of squares, the same in all 16 lanes of the row (every
+// 16-lane row that calls it must be whole: DPP reduction).
+__device__ __forceinline__ float head16_ss(uint2 x_a, uint2 x_b) {
+  float xa[4], xb[4];
+  unpack4(x_a, xa); unpack4(x_b, xb);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) ss = fmaf(xa[i], xa[i], ss);
 #pragma unroll
   for (int i = 0; i < 4; ++i) ss = fmaf(xb[i], xb[i], ss);
-  ss = row16_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-  float na[4], nb[4], ra[4], rb[4];
+  return row16_sum(ss);
+}
+
+__device__ __forceinline__ float head16_inv(float ss, float eps) {
+  return 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+}
+
+// Norm and RoPE of one head from unpacked operands and its 1 / rms: g, c, s
+// hold this lane's gain, cos and sin elements 4e..4e+3 in [0..3] and their
+// partners 64+4e.. in [4..7].
+__device__ __forceinline__ void head16_finish(uint2 x_a, uint2 x_b, float inv, const float* g,
+                                              const float* c, const float* s, uint2& oa,
+                                              uint2& ob) {
+  float xa[4], xb[4];
+  unpack4(x_a, xa); unpack4(x_b, xb);
+  const float *ga = g, *gb = g + 4, *ca = c, *cb = c + 4, *sa = s, *sb = s + 4;
+  // Every rounding is done two values per v_cvt_pk_bf16_f32 (round_bf2):
+  // the same bits as one at a time, fewer instructions.
+  float na[4], nb[4], ra[4], rb[4], t0[4], t1[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    na[i] = round_bf(ga[i] * round_bf(xa[i] * inv));
-    nb[i] = round_bf(gb[i] * round_bf(xb[i] * inv));
+  for (int i = 0; i < 4; i += 2) {
+    round_bf2(xa[i] * inv, xa[i + 1] * inv, t0[i], t0[i + 1]);
+    round_bf2(xb[i] * inv, xb[i + 1] * inv, t1[i], t1[i + 1]);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    ra[i] = round_bf(round_bf(na[i] * ca[i]) + round_bf(-nb[i] * sa[i]));
-    rb[i] = round_bf(round_bf(nb[i] * cb[i]) + round_bf(na[i] * sb[i]));
+  for (int i = 0; i < 4; i += 2) {
+    round_bf2(ga[i] * t0[i], ga[i + 1] * t0[i + 1], na[i], na[i + 1]);
+    round_bf2(gb[i] * t1[i], gb[i + 1] * t1[i + 1], nb[i], nb[i + 1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    round_bf2(na[i] * ca[i], na[i + 1] * ca[i + 1], t0[i], t0[i + 1]);
+    round_bf2(-nb[i] * sa[i], -nb[i + 1] * sa[i + 1], t1[i], t1[i + 1]);
+    ra[i] = t0[i] + t1[i];
+    ra[i + 1] = t0[i + 1] + t1[i + 1];
+    round_bf2(nb[i] * cb[i], nb[i + 1] * cb[i + 1], t0[i], t0[i + 1]);
+    round_bf2(na[i] * sb[i], na[i + 1] * sb[i + 1], t1[i], t1[i + 1]);
+    rb[i] = t0[i] + t1[i];
+    rb[i + 1] = t0[i + 1] + t1[i + 1];
   }
   oa = make_uint2(pack_bf2(ra[0], ra[1]), pack_bf2(ra[2], ra[3]));
   ob = make_uint2(pack_bf2(rb[0], rb[1]), pack_bf2(rb[2], rb[3]));
+}
+
+// Norm and RoPE of one head from unpacked operands (16-lane rows whole).
+__device__ __forceinline__ void head16_math_f(uint2 x_a, uint2 x_b, const float* g,
+                                              const float* c, const float* s, float eps,
+                                              uint2& oa, uint2& ob) {
+  head16_finish(x_a, x_b, head16_inv(head16_ss(x_a, x_b), eps), g, c, s, oa, ob);
+}
+
+// All 64 lanes must call this (16-lane DPP reduction).
+__device__ __forceinline__ void head16_math(const Head16& h, float eps, uint2& oa, uint2& ob) {
+  float g[8], c[8], s[8];
+  unpack4(h.ga, g); unpack4(h.gb, g + 4);
+  unpack4(h.ca, c); unpack4(h.cb, c + 4);
+  unpack4(h.sa, s); unpack4(h.sb, s + 4);
+  head16_math_f(h.xa, h.xb, g, c, s, eps, oa, ob);
 }
 
 // Per-lane choice between two kernel arguments (q or k gain, q or k
@@ -120,52 +163,100 @@ struct RopeArgs {
   int B, T, Hq, Hkv;
 };
 
+// One wave per (token, chunk of up to 16 heads): q chunks first, then k
+// chunks, which also move the token's v rows into the cache. The wave loads
+// and unpacks the gain and the token's cos/sin row once; its four 16-lane
+// rows take heads h0 + row + 4j. Heads past the chunk's end recompute a valid
+// head (a 16-lane row must run whole) and store nothing. The launch keeps
+// tokens * chunks below 2^31.
 __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
-  const int lane = threadIdx.x & 63, e = lane & 15;
-  const long q_rows = static_cast<long>(a.B) * a.T * a.Hq;
-  const long total = q_rows + static_cast<long>(a.B) * a.T * a.Hkv;
-  // Rows past the end recompute the last row (a whole 16-lane group must run
-  // the DPP reduction) and store nothing.
-  const long row_raw = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-  const bool live = row_raw < total;
-  const long row = live ? row_raw : total - 1;
-  const bool is_q = row < q_rows;
-  const long r = is_q ? row : row - q_rows;
-  const int heads = is_q ? a.Hq : a.Hkv;
-  const long b = r / (static_cast<long>(a.T) * heads);
-  const int t = static_cast<int>((r / heads) % a.T);
-  const int h = static_cast<int>(r % heads);
+  const int lane = threadIdx.x & 63, e = lane & 15, row = lane >> 4;
+  const unsigned qc = (a.Hq + 15) >> 4, chunks = qc + ((a.Hkv + 15) >> 4);
+  const unsigned w = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned tok = w / chunks;
+  if (tok >= static_cast<unsigned>(a.B) * static_cast<unsigned>(a.T)) return;
+  const unsigned c = w - tok * chunks;
+  const unsigned b = tok / static_cast<unsigned>(a.T);
+  const int t = static_cast<int>(tok - b * static_cast<unsigned>(a.T));
+  const bool is_q = c < qc;
+  const int nh = is_q ? a.Hq : a.Hkv;
+  const int h0 = static_cast<int>(is_q ? c : c - qc) * 16;
+  const int nj = nh - h0 >= 16 ? 4 : (nh - h0 + 3) / 4;  // passes of the four rows
   // Positions are only read when they select the rope row or the cache slot.
   const int64_t p = (a.rope_by_pos || a.keys) ? a.pos[t] : t;
   const long rr = a.rope_by_pos ? p : t;
-  const bool rope_ok = rr >= 0 && rr < a.rope_rows;
-  const long ri = rope_ok ? rr : 0;
-  const bf16_t* src = is_q ? a.q + b * a.q_sb + t * a.q_st + h * D
-                           : a.k + b * a.k_sb + t * a.k_st + h * D;
-  Head16 hd;
-  head16_load(src, pick_gain(a.qg, a.kg, !is_q), a.cos + ri * a.rope_st, a.sin + ri * a.rope_st, e, hd);
-  uint2 oa, ob;
-  head16_math(hd, is_q ? sgpr_f32(a.q_eps) : sgpr_f32(a.k_eps), oa, ob);
-  if (!live || !rope_ok) return;
-  if (is_q) {
-    bf16_t* dst = a.out_q + ((b * a.T + t) * a.Hq + h) * D;
-    *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
-    *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
-    return;
+  if (rr < 0 || rr >= a.rope_rows) return;  // no rope row: the token stores nothing
+  const bool append = !is_q && a.keys && p >= 0 && p < a.cap;
+
+  const bf16_t* src = is_q ? a.q + b * a.q_sb + t * a.q_st : a.k + b * a.k_sb + t * a.k_st;
+  const bf16_t* vsrc = a.v + b * a.v_sb + t * a.v_st;
+  uint2 xa[4], xb[4], va[4], vb[4];
+  int hh[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = h0 + row + 4 * j;
+    hh[j] = h;
+    if (j < nj) {  // wave-uniform
+      const int hc = h < nh ? h : nh - 1;
+      xa[j] = load_stream8(src + hc * D + 4 * e);  // read once: streaming loads
+      xb[j] = load_stream8(src + hc * D + 64 + 4 * e);
+      if (append) {
+        va[j] = load_stream8(vsrc + hc * D + 4 * e);
+        vb[j] = load_stream8(vsrc + hc * D + 64 + 4 * e);
+      }
+    }
   }
-  if (a.out_k) {
-    bf16_t* dst = a.out_k + ((b * a.T + t) * a.Hkv + h) * D;
-    *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
-    *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
-  }
-  if (a.keys && p >= 0 && p < a.cap) {
-    const long slot = ((b * a.Hkv + h) * a.cap + p) * D;
-    *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
-    *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
-    const bf16_t* vs = a.v + b * a.v_sb + t * a.v_st + h * D;
-    *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = *reinterpret_cast<const uint2*>(vs + 4 * e);
-    *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) =
-        *reinterpret_cast<const uint2*>(vs + 64 + 4 * e);
+  const bf16_t* gain = is_q ? a.qg : a.kg;
+  const bf16_t* cs = a.cos + rr * a.rope_st;
+  const bf16_t* sn = a.sin + rr * a.rope_st;
+  float g[8], co[8], si[8];
+  unpack4(*reinterpret_cast<const uint2*>(gain + 4 * e), g);
+  unpack4(*reinterpret_cast<const uint2*>(gain + 64 + 4 * e), g + 4);
+  unpack4(*reinterpret_cast<const uint2*>(cs + 4 * e), co);
+  unpack4(*reinterpret_cast<const uint2*>(cs + 64 + 4 * e), co + 4);
+  unpack4(*reinterpret_cast<const uint2*>(sn + 4 * e), si);
+  unpack4(*reinterpret_cast<const uint2*>(sn + 64 + 4 * e), si + 4);
+  const float eps = is_q ? a.q_eps : a.k_eps;
+
+  // The four passes' 1 / rms from one evaluation: lane e of a row holds pass
+  // e & 3's sum of squares, and quad_perm [j,j,j,j] hands pass j's result
+  // back to every lane of the row (same bits as one evaluation per pass).
+  float ssj[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ssj[j] = j < nj ? head16_ss(xa[j], xb[j]) : 1.0f;
+  const int js = e & 3;
+  const float sel = js == 0 ? ssj[0] : js == 1 ? ssj[1] : js == 2 ? ssj[2] : ssj[3];
+  const float invs = head16_inv(sel, eps);
+  float invj[4];
+  invj[0] = dpp<0x00>(invs);
+  invj[1] = dpp<0x55>(invs);
+  invj[2] = dpp<0xAA>(invs);
+  invj[3] = dpp<0xFF>(invs);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j >= nj) break;  // wave-uniform
+    const int h = hh[j];
+    uint2 oa, ob;
+    head16_finish(xa[j], xb[j], invj[j], g, co, si, oa, ob);
+    if (h >= nh) continue;
+    if (is_q) {
+      bf16_t* dst = a.out_q + (static_cast<long>(tok) * a.Hq + h) * D;
+      *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
+      continue;
+    }
+    if (a.out_k) {
+      bf16_t* dst = a.out_k + (static_cast<long>(tok) * a.Hkv + h) * D;
+      *reinterpret_cast<uint2*>(dst + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(dst + 64 + 4 * e) = ob;
+    }
+    if (append) {
+      const long slot = ((static_cast<long>(b) * a.Hkv + h) * a.cap + p) * D;
+      *reinterpret_cast<uint2*>(a.keys + slot + 4 * e) = oa;
+      *reinterpret_cast<uint2*>(a.keys + slot + 64 + 4 * e) = ob;
+      *reinterpret_cast<uint2*>(a.values + slot + 4 * e) = va[j];
+      *reinterpret_cast<uint2*>(a.values + slot + 64 + 4 * e) = vb[j];
+    }
   }
 }
 
@@ -1921,8 +2012,10 @@ extern "C" int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, co
   a.out_q = static_cast<bf16_t*>(out_q); a.out_k = static_cast<bf16_t*>(out_k);
   a.B = static_cast<int>(B); a.T = static_cast<int>(T);
   a.Hq = static_cast<int>(Hq); a.Hkv = static_cast<int>(Hkv);
-  const long total = B * T * (Hq + Hkv);
-  hipLaunchKernelGGL(norm_rope_cache_kernel, dim3((total + 15) / 16), dim3(kBlock), 0,
+  // One wave per (token, 16-head chunk), four waves per block.
+  const int64_t waves = B * T * ((Hq + 15) / 16 + (Hkv + 15) / 16);
+  if (waves >= (int64_t{1} << 31)) return HTN_EUNSUPPORTED;
+  hipLaunchKernelGGL(norm_rope_cache_kernel, dim3((waves + 3) / 4), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), a);
   return launch_status();
 }

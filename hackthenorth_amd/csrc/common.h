@@ -34,10 +34,37 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+// bf16(g * sigmoid(g)) from the hardware exp2 and reciprocal: with
+// t = e^-|g| <= 1, sigmoid(g) = 1 / (1 + t) for g >= 0 and t / (1 + t)
+// otherwise, so the reciprocal's argument stays in [1, 2] and nothing
+// overflows. About 2 ulp in fp32 for |g| < 8 before the bf16 rounding (the
+// exponent argument's own rounding adds |g| * 2^-24 relative beyond that).
+__device__ __forceinline__ float silu_bf(float g) {
+  const float t = __builtin_amdgcn_exp2f(-fabsf(g) * 1.4426950408889634f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + t);
+  return round_bf(g * (g >= 0.f ? r : t * r));
+}
+
 // Two roundings in one v_cvt_pk_bf16_f32: lo in bits 0-15, hi in 16-31.
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+// Streaming (nontemporal) 16- and 8-byte loads, for data read exactly once.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+}
+__device__ __forceinline__ uint2 load_stream8(const void* p) {
+  return __builtin_bit_cast(uint2, __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
+}
+
+// round_bf of two values through one conversion.
+__device__ __forceinline__ void round_bf2(float a, float b, float& ra, float& rb) {
+  const uint32_t w = pack_bf2(a, b);
+  ra = bf_lo(w);
+  rb = bf_hi(w);
 }
 
 // 8 bf16 in a uint4 -> fp32 dot with 8 fp32 values.

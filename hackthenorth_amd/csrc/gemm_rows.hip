@@ -50,10 +50,7 @@ struct RowsArgs {
 constexpr long kAlign = 256;
 long align_up(long v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-__device__ __forceinline__ float silu_mul_bf(float g, float u) {
-  const float sig = 1.0f / (1.0f + expf(-g));
-  return round_bf(g * sig) * u;
-}
+__device__ __forceinline__ float silu_mul_bf(float g, float u) { return silu_bf(g) * u; }
 
 // The 16 bytes of x (row m, k .. k+7) as an A fragment; rows past M and
 // invalid steps give zeros.

@@ -95,10 +95,7 @@ struct GemvArgs {
 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  // bf16(bf16(g * sigmoid(g)) * u), sigmoid = 1 / (1 + exp(-g)), each op rounded in fp32.
-  float sig = 1.0f / (1.0f + expf(-g));
-  float act = round_bf(g * sig);
-  return act * u;
+  return silu_bf(g) * u;  // bf16(silu(g)) * u; the caller rounds the product
 }
 
 // Greedy head, stage 1: the block's best (logit, id) key goes to its own slot

@@ -204,6 +204,35 @@ def test_norm_rope_cache_matches_oracle_and_keeps_other_slots(batch, tokens):
         close(rk, exp_k)
 
 
+@pytest.mark.parametrize("q_heads,kv_heads", [(20, 5), (3, 1), (48, 16)])
+def test_norm_rope_cache_ragged_head_counts(q_heads, kv_heads):
+    # Head counts that leave part-filled 16-head chunks (heads past a chunk's
+    # end recompute a valid head and must store nothing).
+    batch, tokens, cap = 2, 3, 9
+    qg, kg = nrm(24, (128,)), nrm(25, (128,))
+    cos_t, sin_t = Q.rope_tables(16, 128, 1e6)
+    positions = torch.tensor([1, 4, 8])
+    cos, sin = cos_t[positions][None], sin_t[positions][None]
+    width = (q_heads + 2 * kv_heads) * 128
+    packed = nrm(26, (batch, tokens, width))
+    keys = torch.full((batch, kv_heads, cap, 128), -7.0, dtype=torch.bfloat16)
+    values = torch.full_like(keys, 7.0)
+    kd, vd = cuda(keys), cuda(values)
+    split = (q_heads * 128, kv_heads * 128, kv_heads * 128)
+    q, k, v = (t.view(batch, tokens, -1, 128) for t in cuda(packed).split(split, -1))
+    out_q, _, _ = F.norm_rope_cache(q, k, v, _norm(qg), _norm(kg), cuda(cos), cuda(sin),
+                                    kd, vd, cuda(positions))
+    eq, ek, ev = (t.view(batch, tokens, -1, 128) for t in packed.split(split, -1))
+    close(out_q, Q.norm_rope(eq, qg, cos[:, :, None], sin[:, :, None], 1e-6).transpose(1, 2))
+    keys[:, :, positions] = Q.norm_rope(ek, kg, cos[:, :, None], sin[:, :, None], 1e-6).transpose(1, 2)
+    values[:, :, positions] = ev.transpose(1, 2)
+    close(kd, keys)
+    assert bits_equal(vd, values)
+    untouched = torch.ones(cap, dtype=torch.bool)
+    untouched[positions] = False
+    assert bits_equal(kd[:, :, untouched], keys[:, :, untouched])
+
+
 ATTN_CASES = [(1, 1, 0, 129), (1, 4, 63, 513), (4, 4, 126, 257), (1, 1, 2047, 2304),
               (1, 5, 4091, 4100), (2, 1, 700, 8200),
               # one query per sequence: a tile boundary, batches, the last slot
