@@ -58,6 +58,9 @@ SIGNATURES = {
                               _I64, _I64, _I64, _I64, _P, _P],
     "htn_prologue_attention": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64, _I,
                                _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P],
+    "htn_prologue_attention_prefetch": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64,
+                                        _I, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P,
+                                        _I64, _I64, _I, _P],
     "htn_xcc_ids": [_P, _I64, _P],
     "htn_attention_merge_in_kernel": [],
 }

@@ -278,7 +278,34 @@ struct AttnArgs {
   int mfma;             // LDS-staged kernel: tiles on the matrix cores
   float scale;
   unsigned* done;       // arrival counters: XCD-affine grid, in-kernel merge (else null)
+  // Blocks from attn_blocks on read the next projection's weights (pf_units
+  // spans of pf_unit_bytes; span u is multiplied by GEMV blocks on the XCD of
+  // attention blocks with index u mod 8) so they wait in that XCD's L2.
+  const unsigned char* pf;
+  long pf_units;
+  int pf_unit_bytes, pf_per_class, attn_blocks;
 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Prefetch role of the blocks past the attention grid: LDS-direct loads of
+// the block's spans into its (otherwise unused) staging LDS, nothing
+// multiplied or stored; the loads only have to pass through the XCD's L2.
+// Every load has landed before the block ends (its LDS is then released).
+__device__ __forceinline__ void prefetch_next(const AttnArgs& a, unsigned char* lds) {
+  const int p = static_cast<int>(blockIdx.x) - a.attn_blocks;
+  const int cls = p & 7, q = p >> 3;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  lds_void_t* dst = (lds_void_t*)(lds + wave * 1024);
+  for (long u = cls + 8L * q; u < a.pf_units; u += 8L * a.pf_per_class) {
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.pf + u * a.pf_unit_bytes,
+                                                  static_cast<uint32_t>(a.pf_unit_bytes));
+    for (int o = wave * 1024; o < a.pf_unit_bytes; o += kBlock * 16)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, lane * 16, o, 0, 0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 // Block coordinates (split s, kv head, batch). With the in-kernel merge the
 // grid is one-dimensional: block L runs on XCD L % 8 (round-robin dispatch;
@@ -922,7 +949,6 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
 constexpr int kLdsWaveTile = 2 * 16 * D * 2;               // K + V bytes of one wave's 16 slots
 constexpr int kLdsTile = kLdsWaveTile * (kBlock / kWave);  // 32 KB per 64-slot tile
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -974,6 +1000,10 @@ template <int ROWS, int PRO, int RING>
 __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
+    prefetch_next(a, ring);
+    return;
+  }
   __shared__ uint32_t qs[ROWS * D / 2];
   __shared__ float wm[kBlock / kWave][ROWS], wl[kBlock / kWave][ROWS];
   __shared__ float wacc[kBlock / kWave][ROWS][D];
@@ -1348,6 +1378,10 @@ template <int ROWS, int PRO, int RING>
 __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
+    prefetch_next(a, ring);
+    return;
+  }
   // MQ: several queries per sequence (16 or 32 rows = heads x queries, each
   // with its own position); otherwise one query, up to 8 heads per kv head.
   constexpr bool MQ = ROWS > 8;
@@ -1772,7 +1806,7 @@ namespace {
 dim3 split_grid(const AttnArgs& a) {
   if (!a.done) return dim3(a.splits, a.Hkv, a.B);
   const long pairs = static_cast<long>(a.B) * a.Hkv;
-  return dim3(static_cast<unsigned>(8 * ((pairs + 7) / 8) * a.splits));
+  return dim3(static_cast<unsigned>(8 * ((pairs + 7) / 8) * a.splits + (a.pf ? 8 * a.pf_per_class : 0)));
 }
 
 template <int ROWS, int TILES>
@@ -1880,7 +1914,23 @@ bool xcd_affine_merge() {
   return state[dev] == 1;
 }
 
-int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
+// The projection that reads this attention's output, for the prefetch blocks.
+struct NextWeights {
+  const void* w;
+  long n, k;
+  int format;
+};
+
+// Prefetch blocks per XCD, and the bytes they read into each XCD's 4 MB L2
+// (measured on 0.6B and 8B decode steps: 8 blocks beat 2, 4, 16 and 32 -- few
+// blocks outlast the attention, many crowd its loads -- and 3 MB per XCD beat
+// all of the 8B's 4 MB, 2 MB and 1 MB). With the staging ring every block
+// holds at least 32 KB of LDS, so they run on CUs the attention leaves free.
+constexpr int kPrefetchPerXcd = 8;
+constexpr long kPrefetchXcdBytes = 3L << 20;
+
+int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
+                  const NextWeights* next = nullptr) {
   const int rows = a.G * a.Q;
   if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
     return HTN_EUNSUPPORTED;
@@ -1960,6 +2010,25 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st) {
       out_pairs && xcd_affine_merge())
     a.done = reinterpret_cast<unsigned*>(sbase);
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
+  // Prefetch of the next projection's weights: only with the XCD-affine grid
+  // of the LDS-staged kernels (one dimension, eight block columns) and a
+  // GEMV grid of whole columns, so span u and its GEMV block share an XCD.
+  a.pf = nullptr;
+  long gemv_blocks = 0;
+  int gemv_rows = 0;
+  if (next && next->w && a.done && a.ring > 0 && !a.stream &&
+      gemv_plain_layout(next->n, next->k, next->format, &gemv_blocks, &gemv_rows) &&
+      gemv_blocks % 8 == 0) {
+    const long row_bytes = next->k * (next->format == 0 ? 2 : 1);
+    a.pf = static_cast<const unsigned char*>(next->w);
+    a.pf_unit_bytes = static_cast<int>(gemv_rows * row_bytes);
+    const long units = next->n / gemv_rows;  // whole spans only
+    const long cap_units = 8 * kPrefetchXcdBytes / a.pf_unit_bytes;
+    a.pf_units = units < cap_units ? units : cap_units;
+    a.pf_per_class = kPrefetchPerXcd;
+    const long pairs = static_cast<long>(a.B) * a.Hkv;
+    a.attn_blocks = static_cast<int>(8 * ((pairs + 7) / 8) * a.splits);
+  }
   if (a.mfma && a.Q > 1) launch_mfma_rows(a, st);
   else if (rows <= 1) launch_partial<1>(fused, a, st);
   else if (rows <= 2) launch_partial<2>(fused, a, st);
@@ -2043,14 +2112,14 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
   return run_attention(false, a, scratch, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off,
-                                      int64_t v_off, const void* q_gain, const void* k_gain,
-                                      float q_eps, float k_eps, const void* cos, const void* sin,
-                                      int64_t rope_st, int64_t rope_rows, int rope_by_position,
-                                      void* keys, void* values, int64_t cap,
-                                      const int64_t* positions, void* out, int64_t B,
-                                      int64_t Hkv, int64_t groups, void* scratch,
-                                      htn_stream_t stream) {
+namespace {
+int prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off,
+                       const void* q_gain, const void* k_gain, float q_eps, float k_eps,
+                       const void* cos, const void* sin, int64_t rope_st, int64_t rope_rows,
+                       int rope_by_position, void* keys, void* values, int64_t cap,
+                       const int64_t* positions, void* out, int64_t B, int64_t Hkv,
+                       int64_t groups, void* scratch, const NextWeights* next,
+                       htn_stream_t stream) {
   if (!qkv || !q_gain || !k_gain || !cos || !sin || !keys || !values || !positions || !out)
     return HTN_EINVAL;
   if (Hkv <= 0 || groups <= 0 || rope_rows <= 0) return HTN_EINVAL;
@@ -2070,7 +2139,37 @@ extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k
   a.B = static_cast<int>(B); a.Hkv = static_cast<int>(Hkv); a.G = static_cast<int>(groups);
   a.Hq = static_cast<int>(Hkv * groups); a.Q = 1;
   a.o_sh = D; a.o_st = D; a.o_sb = static_cast<long>(a.Hq) * D;  // out [B, Hq, 128]
-  return run_attention(true, a, scratch, static_cast<hipStream_t>(stream));
+  return run_attention(true, a, scratch, static_cast<hipStream_t>(stream), next);
+}
+}  // namespace
+
+extern "C" int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off,
+                                      int64_t v_off, const void* q_gain, const void* k_gain,
+                                      float q_eps, float k_eps, const void* cos, const void* sin,
+                                      int64_t rope_st, int64_t rope_rows, int rope_by_position,
+                                      void* keys, void* values, int64_t cap,
+                                      const int64_t* positions, void* out, int64_t B,
+                                      int64_t Hkv, int64_t groups, void* scratch,
+                                      htn_stream_t stream) {
+  return prologue_attention(qkv, qkv_sb, k_off, v_off, q_gain, k_gain, q_eps, k_eps, cos, sin,
+                            rope_st, rope_rows, rope_by_position, keys, values, cap, positions,
+                            out, B, Hkv, groups, scratch, nullptr, stream);
+}
+
+extern "C" int htn_prologue_attention_prefetch(
+    const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off, const void* q_gain,
+    const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+    int64_t rope_st, int64_t rope_rows, int rope_by_position, void* keys, void* values,
+    int64_t cap, const int64_t* positions, void* out, int64_t B, int64_t Hkv, int64_t groups,
+    void* scratch, const void* next_w, int64_t next_n, int64_t next_k, int next_format,
+    htn_stream_t stream) {
+  if (!next_w || next_n <= 0 || next_k <= 0 ||
+      (next_format != 0 && next_format != HTN_WEIGHT_INT8 && next_format != HTN_WEIGHT_FP8_E4M3))
+    return HTN_EINVAL;
+  const NextWeights next{next_w, next_n, next_k, next_format};
+  return prologue_attention(qkv, qkv_sb, k_off, v_off, q_gain, k_gain, q_eps, k_eps, cos, sin,
+                            rope_st, rope_rows, rope_by_position, keys, values, cap, positions,
+                            out, B, Hkv, groups, scratch, &next, stream);
 }
 
 namespace htn {

@@ -201,6 +201,12 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
 // ------------------------------------------------------------------ host helpers
 
 int device_cus();  // compute units of the current device (cached per device)
+// Grid of the one-token GEMV over n rows of k weights (format 0 for bf16, or
+// HTN_WEIGHT_INT8 / HTN_WEIGHT_FP8_E4M3) without the RMSNorm prologue and without SwiGLU: its block count and
+// the rows each block takes per grid step (block b multiplies rows
+// [b * rows, (b + 1) * rows), then the same span blocks * rows further on).
+// False when the weights take the scalar path.
+bool gemv_plain_layout(long n, long k, int format, long* blocks, int* rows);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }

@@ -530,6 +530,25 @@ int dispatch(GemvArgs& a, hipStream_t st) {
   return launch_vec<1, S, 8, NORM, EPI, WF>(a, st);
 }
 
+}  // namespace
+
+bool gemv_plain_layout(long n, long k, int format, long* blocks, int* rows) {
+  const int epv = format == WF_BF16 ? Fmt<WF_BF16>::kPerVec : Fmt<WF_INT8>::kPerVec;
+  if (n <= 0 || k <= 0 || k > kMaxK || k % epv != 0) return false;
+  // Mirrors dispatch() for S = 1 and no prologue.
+  const int chunks = static_cast<int>((k / epv + 63) / 64);
+  const bool many_rows = n >= 4 * kWavesPerCu * device_cus();
+  int r = 1;
+  if (format != WF_BF16 && chunks == 1) r = many_rows ? 4 : 1;
+  else if (format != WF_BF16 && chunks > 8) r = 2;
+  else if (chunks <= 2) r = many_rows ? 4 : 1;
+  *blocks = grid_for((n + r - 1) / r, 8);
+  *rows = 4 * r;
+  return true;
+}
+
+namespace {
+
 bool bad_sizes(int64_t n, int64_t k) { return n <= 0 || k <= 0 || k > kMaxK || n > (1L << 31); }
 
 bool bad_format(int format) { return format != WF_INT8 && format != WF_FP8; }

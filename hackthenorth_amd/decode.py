@@ -109,7 +109,8 @@ def decode_layer(model, i, h, cache, position, rotary, rope=None):
     if rope is not None:
         a = prologue_attention(packed, layer.q_norm, layer.k_norm, rope[0], rope[1],
                                cache.keys[i], cache.values[i], position,
-                               c.num_key_value_heads, groups, q_width, q_width + k_width)
+                               c.num_key_value_heads, groups, q_width, q_width + k_width,
+                               next_weight=layer.o_weight)
     else:
         a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
                              cache.keys[i], cache.values[i], position,

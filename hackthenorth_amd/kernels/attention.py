@@ -9,6 +9,7 @@ variant appends the newest k/v to the cache, as the reference's does).
 import torch
 
 from .. import _lib
+from ..quant import QuantizedWeight
 
 
 # (device index, stream handle) -> zero-initialised scratch buffers, newest last.
@@ -70,7 +71,7 @@ def grouped_attention(q, k, v, positions, out=None):
 
 
 def _prologue(qkv, q_norm, k_norm, cos, sin, by_position, keys, values, positions, kv_heads,
-              groups, k_offset, v_offset):
+              groups, k_offset, v_offset, next_weight=None):
     batch, width = qkv.shape[0], qkv.shape[-1]
     if qkv.numel() != batch * width or qkv.stride(-1) != 1 or qkv.dtype != torch.bfloat16:
         raise ValueError("qkv must be a bf16 [B, 1, width] packed projection")
@@ -88,25 +89,41 @@ def _prologue(qkv, q_norm, k_norm, cos, sin, by_position, keys, values, position
     rope_rows = cos.numel() // _lib.HEAD_DIM
     out = torch.empty((batch, heads, 1, _lib.HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
     scratch = _scratch(qkv.device, batch, heads, 1, keys.shape[2])
-    _lib.call("htn_prologue_attention", _lib.ptr(qkv), qkv.stride(0), k_offset, v_offset,
-              _lib.ptr(q_norm.weight), _lib.ptr(k_norm.weight), float(q_norm.variance_epsilon),
-              float(k_norm.variance_epsilon), _lib.ptr(cos), _lib.ptr(sin), _lib.HEAD_DIM,
-              rope_rows, int(by_position), _lib.ptr(keys), _lib.ptr(values), keys.shape[2],
-              _lib.ptr(positions), _lib.ptr(out), batch, kv_heads, groups, _lib.ptr(scratch),
-              _lib.stream(qkv.device))
+    args = (_lib.ptr(qkv), qkv.stride(0), k_offset, v_offset,
+            _lib.ptr(q_norm.weight), _lib.ptr(k_norm.weight), float(q_norm.variance_epsilon),
+            float(k_norm.variance_epsilon), _lib.ptr(cos), _lib.ptr(sin), _lib.HEAD_DIM,
+            rope_rows, int(by_position), _lib.ptr(keys), _lib.ptr(values), keys.shape[2],
+            _lib.ptr(positions), _lib.ptr(out), batch, kv_heads, groups, _lib.ptr(scratch))
+    if next_weight is None:
+        _lib.call("htn_prologue_attention", *args, _lib.stream(qkv.device))
+        return out
+    # The projection that reads this output: idle CUs load its weights into
+    # the L2 of the XCDs that will multiply them while the attention runs.
+    if isinstance(next_weight, QuantizedWeight):
+        data, fmt = next_weight.data, next_weight.code
+    else:
+        data, fmt = next_weight, 0
+    if data.dim() != 2 or not data.is_contiguous():
+        raise ValueError("next_weight must be a contiguous [N, K] weight")
+    _lib.require_gpu(data)
+    _lib.call("htn_prologue_attention_prefetch", *args, _lib.ptr(data), data.shape[0],
+              data.shape[1], fmt, _lib.stream(qkv.device))
     return out
 
 
 def prologue_attention(qkv, q_norm, k_norm, cos, sin, keys, values, positions,
-                       kv_heads, groups, k_offset, v_offset):
+                       kv_heads, groups, k_offset, v_offset, next_weight=None):
     """Single-token decode attention with norm/rope/cache-write fused in (attention.py:162).
 
     qkv is the packed (batch, 1, width) projection; cos/sin the selected
     [1, 1, 128] rows. Writes the newest K/V into slot positions[0] and
-    returns [batch, heads, 1, 128].
+    returns [batch, heads, 1, 128]. `next_weight`, the output projection's
+    weight (bf16 or QuantizedWeight), is read into the L2 of the XCDs whose
+    GEMV blocks will multiply it, by blocks on CUs the attention leaves idle;
+    results are the same with or without it.
     """
     return _prologue(qkv, q_norm, k_norm, cos, sin, False, keys, values, positions, kv_heads,
-                     groups, k_offset, v_offset)
+                     groups, k_offset, v_offset, next_weight)
 
 
 def decode_attention(qkv, q_norm, k_norm, cos_table, sin_table, keys, values, position,

@@ -258,6 +258,24 @@ int htn_prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64
                            const int64_t* positions, void* out, int64_t B, int64_t Hkv,
                            int64_t groups, void* scratch, htn_stream_t stream);
 
+/* htn_prologue_attention, plus the weight of the projection that reads its
+ * output (next_n x next_k, format 0 = bf16, HTN_WEIGHT_INT8 or
+ * HTN_WEIGHT_FP8_E4M3; row scales are not read): while the attention runs,
+ * blocks on CUs it leaves idle read up to 3 MB of those weights per XCD into
+ * the L2 of the XCD whose GEMV blocks will multiply them (one-token GEMV
+ * grid, equal block index mod 8). Results are identical to
+ * htn_prologue_attention; only the following projection gets faster. Used
+ * with the XCD-affine split grid only (otherwise no prefetch).
+ * Replaces prologue_attention(...), kernels/attention.py:162, in the decode
+ * step (the reference has no such prefetch). */
+int htn_prologue_attention_prefetch(
+    const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off, const void* q_gain,
+    const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+    int64_t rope_st, int64_t rope_rows, int rope_by_position, void* keys, void* values,
+    int64_t cap, const int64_t* positions, void* out, int64_t B, int64_t Hkv, int64_t groups,
+    void* scratch, const void* next_w, int64_t next_n, int64_t next_k, int next_format,
+    htn_stream_t stream);
+
 /* Diagnostics of the in-kernel attention merge; no counterpart in the
  * reference. htn_xcc_ids writes, for each block b < blocks of a
  * one-dimensional grid, the XCD it ran on (hardware register XCC_ID), so a

@@ -22,6 +22,7 @@ from hackthenorth_amd.kernels.down import down_residual
 from hackthenorth_amd.kernels.embed import embed_gather
 from hackthenorth_amd.kernels import rng as DR
 from hackthenorth_amd.model import Norm
+from hackthenorth_amd.quant import QuantizedWeight
 
 pytestmark = pytest.mark.gpu
 ATOL = RTOL = 2e-2
@@ -300,6 +301,29 @@ def test_decode_attention_pair_counts_match_oracle(batch, heads, kv_heads, posit
     positions = torch.tensor([position])
     actual = A.grouped_attention(cuda(q.contiguous()), cuda(k), cuda(v), cuda(positions))
     close(actual, Q.attention(q, k, v, positions))
+
+
+@pytest.mark.parametrize("width,n", [(4096, 4096), (2048, 1024)])
+def test_prologue_attention_prefetch_keeps_results(width, n):
+    # The prefetch blocks only read the next projection's weights: output and
+    # cache writes are bit-identical with and without them (8B and 0.6B O shapes,
+    # plus an 8-bit weight).
+    heads, kv, cap, p = width // 128, 8, 2300, 2047
+    qg, kg = _norm(nrm(44, (128,))), _norm(nrm(45, (128,)))
+    cos_t, sin_t = Q.rope_tables(cap, 128, 1e6)
+    cos, sin = cuda(cos_t[p:p + 1][None]), cuda(sin_t[p:p + 1][None])
+    packed = cuda(nrm(46, (1, 1, width + 2 * kv * 128)))
+    keys, values = cuda(nrm(47, (1, kv, cap, 128))), cuda(nrm(48, (1, kv, cap, 128)))
+    pos = torch.tensor([p], dtype=torch.int64, device="cuda")
+    w = cuda(nrm(49, (n, width)))
+    outs = []
+    for nxt in (None, w, QuantizedWeight.quantize(w, "int8")):
+        k2, v2 = keys.clone(), values.clone()
+        out = A.prologue_attention(packed, qg, kg, cos, sin, k2, v2, pos, kv, heads // kv, width,
+                                   width + kv * 128, next_weight=nxt)
+        outs.append((out.cpu(), k2.cpu(), v2.cpu()))
+    for o, k2, v2 in outs[1:]:
+        assert bits_equal(o, outs[0][0]) and bits_equal(k2, outs[0][1]) and bits_equal(v2, outs[0][2])
 
 
 def test_split_merge_counters_rearm_across_calls():
