@@ -35,6 +35,7 @@ SIGNATURES = {
     "htn_fill_uniform_f32": [_P, _I64, _U64, _U64, _F, _F, _P],
     "htn_fill_weights_w8": [_P, _I64, _U64, _U64, _I, _P],
     "htn_embed_gather": [_P, _I64, _P, _I64, _I64, _P, _P],
+    "htn_embed_gather_pair": [_P, _I64, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _P, _P],
     "htn_rms_norm": [_P, _I64, _P, _P, _I64, _I64, _F, _P],
     "htn_add_rms_norm": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
     "htn_swiglu": [_P, _I64, _P, _I64, _P, _I64, _I64, _P],

@@ -152,21 +152,29 @@ __global__ __launch_bounds__(kBlock) void swiglu_scalar(const bf16_t* __restrict
 // the wave's rows, up to kEmbedPieces per lane in flight before the first
 // store. Ids outside [0, vocab) give zero rows.
 constexpr int kEmbedRows = 4, kEmbedPieces = 8;
-__global__ __launch_bounds__(kBlock) void embed_vec(const int64_t* __restrict__ ids, long count,
-                                                    const bf16_t* __restrict__ table, long vocab,
-                                                    int hidden, bf16_t* __restrict__ out) {
+
+struct EmbedJob {
+  const int64_t* ids;
+  long count;
+  const bf16_t* table;
+  long vocab;
+  int hidden;
+  bf16_t* out;
+};
+
+// Wave w of a job gathers ids 4w .. 4w + 3.
+__device__ __forceinline__ void embed_wave(const EmbedJob& j, long w) {
   const int lane = threadIdx.x & 63;
-  const long first = (static_cast<long>(blockIdx.x) * (kBlock / kWave) +
-                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * kEmbedRows;
-  if (first >= count) return;
-  const int nrows = count - first < kEmbedRows ? static_cast<int>(count - first) : kEmbedRows;
+  const long first = w * kEmbedRows;
+  if (first >= j.count) return;
+  const int nrows = j.count - first < kEmbedRows ? static_cast<int>(j.count - first) : kEmbedRows;
   int64_t id[kEmbedRows];
 #pragma unroll
   for (int r = 0; r < kEmbedRows; ++r) {
-    const int64_t v = r < nrows ? ids[first + r] : -1;
-    id[r] = v >= 0 && v < vocab ? v : -1;
+    const int64_t v = r < nrows ? j.ids[first + r] : -1;
+    id[r] = v >= 0 && v < j.vocab ? v : -1;
   }
-  const unsigned nv = static_cast<unsigned>(hidden) >> 3;
+  const unsigned nv = static_cast<unsigned>(j.hidden) >> 3;
   const unsigned items = nv * nrows;
   for (unsigned p0 = 0; p0 < items; p0 += 64 * kEmbedPieces) {
     uint4 val[kEmbedPieces];
@@ -178,13 +186,27 @@ __global__ __launch_bounds__(kBlock) void embed_vec(const int64_t* __restrict__ 
       cc[k] = i - rr[k] * nv;
       const int64_t idr = rr[k] == 0 ? id[0] : rr[k] == 1 ? id[1] : rr[k] == 2 ? id[2] : id[3];
       val[k] = make_uint4(0, 0, 0, 0);
-      if (i < items && idr >= 0) val[k] = *reinterpret_cast<const uint4*>(table + idr * hidden + cc[k] * 8);
+      if (i < items && idr >= 0)
+        val[k] = *reinterpret_cast<const uint4*>(j.table + idr * j.hidden + cc[k] * 8);
     }
 #pragma unroll
     for (int k = 0; k < kEmbedPieces; ++k)
       if (p0 + k * 64 + lane < items)
-        *reinterpret_cast<uint4*>(out + (first + rr[k]) * hidden + cc[k] * 8) = val[k];
+        *reinterpret_cast<uint4*>(j.out + (first + rr[k]) * j.hidden + cc[k] * 8) = val[k];
   }
+}
+
+__global__ __launch_bounds__(kBlock) void embed_vec(EmbedJob j) {
+  embed_wave(j, static_cast<long>(blockIdx.x) * (kBlock / kWave) +
+                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+}
+
+// Two gathers in one launch (the decode step's token row and RoPE row):
+// blocks below split take job a, the rest job b.
+__global__ __launch_bounds__(kBlock) void embed_pair(EmbedJob a, EmbedJob b, unsigned split) {
+  const long w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (blockIdx.x < split) embed_wave(a, static_cast<long>(blockIdx.x) * (kBlock / kWave) + w);
+  else embed_wave(b, static_cast<long>(blockIdx.x - split) * (kBlock / kWave) + w);
 }
 
 __global__ __launch_bounds__(kBlock) void embed_scalar(const int64_t* __restrict__ ids,
@@ -295,6 +317,37 @@ extern "C" int htn_swiglu(const void* gate, int64_t gate_row_stride, const void*
   return launch_status();
 }
 
+namespace {
+long embed_blocks(int64_t count) {
+  return (count + (kBlock / kWave) * kEmbedRows - 1) / ((kBlock / kWave) * kEmbedRows);
+}
+}  // namespace
+
+extern "C" int htn_embed_gather_pair(const int64_t* ids_a, int64_t count_a, const void* table_a,
+                                     int64_t vocab_a, int64_t hidden_a, void* out_a,
+                                     const int64_t* ids_b, int64_t count_b, const void* table_b,
+                                     int64_t vocab_b, int64_t hidden_b, void* out_b,
+                                     htn_stream_t stream) {
+  if (!ids_a || !table_a || !out_a || count_a <= 0 || vocab_a <= 0 || hidden_a <= 0 ||
+      !ids_b || !table_b || !out_b || count_b <= 0 || vocab_b <= 0 || hidden_b <= 0 ||
+      count_a > (1L << 31) || count_b > (1L << 31))
+    return HTN_EINVAL;
+  if (hidden_a % 8 || hidden_b % 8 || !aligned16(table_a) || !aligned16(out_a) ||
+      !aligned16(table_b) || !aligned16(out_b))
+    return HTN_EUNSUPPORTED;
+  const long split = embed_blocks(count_a);
+  hipLaunchKernelGGL(embed_pair, dim3(split + embed_blocks(count_b)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream),
+                     EmbedJob{ids_a, static_cast<long>(count_a), static_cast<const bf16_t*>(table_a),
+                              static_cast<long>(vocab_a), static_cast<int>(hidden_a),
+                              static_cast<bf16_t*>(out_a)},
+                     EmbedJob{ids_b, static_cast<long>(count_b), static_cast<const bf16_t*>(table_b),
+                              static_cast<long>(vocab_b), static_cast<int>(hidden_b),
+                              static_cast<bf16_t*>(out_b)},
+                     static_cast<unsigned>(split));
+  return launch_status();
+}
+
 extern "C" int htn_embed_gather(const int64_t* ids, int64_t count, const void* table,
                                 int64_t vocab, int64_t hidden, void* out, htn_stream_t stream) {
   if (!ids || !table || !out || count <= 0 || vocab <= 0 || hidden <= 0 || count > (1L << 31))
@@ -302,9 +355,10 @@ extern "C" int htn_embed_gather(const int64_t* ids, int64_t count, const void* t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool vec = hidden % 8 == 0 && aligned16(table) && aligned16(out);
   if (vec)
-    hipLaunchKernelGGL(embed_vec, dim3((count + 4 * kEmbedRows - 1) / (4 * kEmbedRows)), dim3(kBlock), 0,
-                       st, ids, static_cast<long>(count), static_cast<const bf16_t*>(table),
-                       static_cast<long>(vocab), static_cast<int>(hidden), static_cast<bf16_t*>(out));
+    hipLaunchKernelGGL(embed_vec, dim3(embed_blocks(count)), dim3(kBlock), 0, st,
+                       EmbedJob{ids, static_cast<long>(count), static_cast<const bf16_t*>(table),
+                                static_cast<long>(vocab), static_cast<int>(hidden),
+                                static_cast<bf16_t*>(out)});
   else
     hipLaunchKernelGGL(embed_scalar, dim3(count), dim3(kBlock), 0, st, ids,
                        static_cast<const bf16_t*>(table), static_cast<long>(vocab),

@@ -18,7 +18,7 @@ import torch
 from ._lib import HEAD_DIM
 from .kernels.attention import decode_attention, grouped_attention, prologue_attention
 from .kernels.down import down_residual
-from .kernels.embed import embed_gather
+from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
@@ -125,8 +125,10 @@ def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=Non
     """Batch-one single-token step through the fused kernels.
 
     `record`, when a list, receives the hidden state after every layer."""
-    h = embed_gather(token_ids.reshape(1), model.embed_weight)
-    rope = rotary.step_row(position)
+    # The token's embedding row and the step's RoPE row: one gather launch.
+    h, row = embed_gather_pair(token_ids.reshape(1), model.embed_weight, position.reshape(1),
+                               rotary.rows)
+    rope = (row[:, :HEAD_DIM], row[:, HEAD_DIM:])
     for i in range(len(model.layers)):
         h = decode_layer(model, i, h, cache, position, rotary, rope)
         if record is not None:

@@ -89,6 +89,16 @@ int htn_fill_weights_w8(void* out, int64_t count, uint64_t seed, uint64_t stream
 int htn_embed_gather(const int64_t* ids, int64_t count, const void* table, int64_t vocab,
                      int64_t hidden, void* out, htn_stream_t stream);
 
+/* Two htn_embed_gather calls in one launch (hidden sizes multiples of 8,
+ * tables and outputs 16-byte aligned, else HTN_EUNSUPPORTED). The decode step
+ * gathers its token row and its RoPE (cos | sin) row this way. Replaces
+ * base.embed_tokens(token_ids), decode.py:81, plus the rotary row lookup of
+ * decode.py:49-67 in one kernel (the reference runs them as separate ops). */
+int htn_embed_gather_pair(const int64_t* ids_a, int64_t count_a, const void* table_a,
+                          int64_t vocab_a, int64_t hidden_a, void* out_a,
+                          const int64_t* ids_b, int64_t count_b, const void* table_b,
+                          int64_t vocab_b, int64_t hidden_b, void* out_b, htn_stream_t stream);
+
 /* ---------------------------------------------------------------- norms */
 
 /* out = bf16(gain * bf16(x * rsqrt(mean(x^2) + eps))) per row.

@@ -169,6 +169,17 @@ def test_greedy_head_matches_oracle_argmax():
     assert G.argmax(cuda(logits)).tolist() == Q.greedy(logits).tolist()
 
 
+def test_embed_gather_pair_equals_two_gathers():
+    from hackthenorth_amd.kernels.embed import embed_gather_pair
+    ta, tb = cuda(nrm(70, (1000, 1024))), cuda(nrm(71, (300, 256)))
+    for ia, ib in (([5], [299]), ([0, 999, -1, 1000, 7], [3]), (list(range(9)), [1, 2, 300])):
+        ida = torch.tensor(ia, dtype=torch.int64, device="cuda")
+        idb = torch.tensor(ib, dtype=torch.int64, device="cuda")
+        oa, ob = embed_gather_pair(ida, ta, idb, tb)
+        assert bits_equal(oa, embed_gather(ida, ta).cpu())
+        assert bits_equal(ob, embed_gather(idb, tb).cpu())
+
+
 def _norm(weight, eps=1e-6):
     return Norm(cuda(weight), eps)
 
