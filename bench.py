@@ -384,7 +384,7 @@ def main():
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
                     choices=("all", "qwen3-8b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
-                             "batched"),
+                             "batched", "per-op"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -411,6 +411,8 @@ def main():
             out = run_draft_speculation(4096, 128, 4, log)
         elif args.section == "batched":
             out = run_batched("qwen3-8b", 512, 32, (1, 4, 16), log)
+        elif args.section == "per-op":
+            out = {"per_op": per_op_microbench()}
         else:
             fmt = "int8" if args.section.endswith("int8") else "fp8_e4m3"
             r = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
