@@ -45,6 +45,10 @@ struct RowsArgs {
   uint64_t* keys;       // argmax: [strips][M]
   int64_t* tokens;      // argmax: [M]
   int M, N, K, KS, steps_per_split;
+  // Residual epilogue fused with the next RMSNorm (K-split finish only):
+  // normed [M][N] = bf16(gain * bf16(y * inv)), the row-wise RMSNorm of y.
+  const bf16_t* ngain; float neps;
+  bf16_t* normed;
 };
 
 constexpr long kAlign = 256;
@@ -203,6 +207,66 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_finish(RowsArgs a) {
   store_out<EPI>(a, m, n, v[0], S > 1 ? v[S - 1] : 0.f);
 }
 
+// K-split finish of the residual epilogue fused with the next RMSNorm: one
+// wave per row m. Lane l owns the row's 8-element vectors l, l + 64, ...: it
+// sums their partials in split order, adds the residual, rounds, stores y and
+// keeps the bf16 y vectors in registers; the wave's sum of squares then
+// normalises them. The summation order of the squares (vector by vector,
+// element by element per lane, then one wave reduction) is the row-wise
+// RMSNorm's, so `normed` is bit-identical to running it on y.
+__global__ __launch_bounds__(kWave) void gemm_rows_finish_norm(RowsArgs a) {
+  constexpr int kMaxVec = 16;  // up to 8192 columns
+  const int lane = threadIdx.x;
+  const int m = blockIdx.x;
+  const int nv = a.N >> 3;
+  uint4 vals[kMaxVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int v = j * 64 + lane;
+    vals[j] = make_uint4(0, 0, 0, 0);
+    if (v < nv) {
+      float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < a.KS; ++ks) {
+        const float4* p =
+            reinterpret_cast<const float4*>(a.part + (static_cast<long>(ks) * a.M + m) * a.N + v * 8);
+        const float4 p0 = p[0], p1 = p[1];
+        t[0] += p0.x; t[1] += p0.y; t[2] += p0.z; t[3] += p0.w;
+        t[4] += p1.x; t[5] += p1.y; t[6] += p1.z; t[7] += p1.w;
+      }
+      float r[8];
+      unpack8(*reinterpret_cast<const uint4*>(a.res + m * a.res_rs + v * 8), r);
+      uint4 yv;
+      yv.x = pack_bf2(round_bf(t[0]) + r[0], round_bf(t[1]) + r[1]);
+      yv.y = pack_bf2(round_bf(t[2]) + r[2], round_bf(t[3]) + r[3]);
+      yv.z = pack_bf2(round_bf(t[4]) + r[4], round_bf(t[5]) + r[5]);
+      yv.w = pack_bf2(round_bf(t[6]) + r[6], round_bf(t[7]) + r[7]);
+      *reinterpret_cast<uint4*>(a.y + m * a.y_rs + v * 8) = yv;
+      vals[j] = yv;
+      float f[8];
+      unpack8(yv, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.N) + a.neps);
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int v = j * 64 + lane;
+    if (v < nv) {
+      float f[8], g[8];
+      unpack8(vals[j], f);
+      unpack8(*reinterpret_cast<const uint4*>(a.ngain + v * 8), g);
+      uint4 o;
+      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+      *reinterpret_cast<uint4*>(a.normed + static_cast<long>(m) * a.N + v * 8) = o;
+    }
+  }
+}
+
 // Per-row argmax over the strips' keys.
 __global__ __launch_bounds__(kBlock) void gemm_rows_argmax(const uint64_t* __restrict__ keys,
                                                           int strips, int M, int64_t* tokens) {
@@ -251,6 +315,8 @@ int launch_w(RowsArgs& a, hipStream_t st) {
   if (launch_status() != HTN_OK) return HTN_ELAUNCH;
   if (EPI == HTN_EPI_ARGMAX) {
     hipLaunchKernelGGL(gemm_rows_argmax, dim3(a.M), dim3(kBlock), 0, st, a.keys, strips, a.M, a.tokens);
+  } else if (a.KS > 1 && EPI == HTN_EPI_RESIDUAL && a.normed) {
+    hipLaunchKernelGGL(gemm_rows_finish_norm, dim3(a.M), dim3(kWave), 0, st, a);
   } else if (a.KS > 1) {
     const long outs = static_cast<long>(a.M) * a.N;
     hipLaunchKernelGGL((gemm_rows_finish<S, EPI>), dim3((outs + kBlock - 1) / kBlock), dim3(kBlock),
@@ -346,4 +412,45 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   a.tokens = tokens;
   if (rows <= 16) return dispatch_epi<1>(a, epilogue, p.waves, st);
   return dispatch_epi<2>(a, epilogue, p.waves, st);
+}
+
+extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w,
+                                           int64_t n, int64_t k, int64_t rows,
+                                           const void* residual, int64_t res_stride, void* y,
+                                           int64_t y_stride, const void* gain, float eps,
+                                           void* normed, void* scratch, htn_stream_t stream) {
+  if (!x || !w || !residual || !y || !gain || !normed || rows <= 0 || rows > kMaxRowsMT ||
+      n <= 0 || k <= 0 || n > (1L << 31))
+    return HTN_EINVAL;
+  const Plan p = plan(rows, n, k, HTN_EPI_RESIDUAL, false);
+  // One wave holds a row of y in registers: 8-element vectors, at most 8192 columns.
+  const bool fused = p.ks > 1 && n % 8 == 0 && n <= 8192 && res_stride % 8 == 0 &&
+                     y_stride % 8 == 0 && aligned16(residual) && aligned16(y) &&
+                     aligned16(gain) && aligned16(normed);
+  if (!fused) {
+    // No K split to finish (or unaligned rows): the residual projection, then
+    // the row-wise RMSNorm of its output.
+    const int rc = htn_gemm_rows(x, x_stride, nullptr, 0.f, w, n, k, rows, HTN_EPI_RESIDUAL,
+                                 residual, res_stride, y, y_stride, nullptr, scratch, stream);
+    if (rc != HTN_OK) return rc;
+    return htn_rms_norm(y, y_stride, gain, normed, rows, n, eps, stream);
+  }
+  if (k % kStep || k > kMaxK || x_stride % 8 || !aligned16(x) || !aligned16(w))
+    return HTN_EUNSUPPORTED;
+  if (!scratch) return HTN_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  RowsArgs a{};
+  a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
+  a.w = static_cast<const bf16_t*>(w);
+  a.res = static_cast<const bf16_t*>(residual); a.res_rs = res_stride;
+  a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
+  a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
+  a.KS = p.ks;
+  a.steps_per_split = (a.K / kStep + a.KS - 1) / a.KS;
+  a.part = static_cast<float*>(scratch);
+  a.ngain = static_cast<const bf16_t*>(gain);
+  a.neps = eps;
+  a.normed = static_cast<bf16_t*>(normed);
+  if (rows <= 16) return launch<1, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+  return launch<2, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
 }

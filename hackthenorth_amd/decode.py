@@ -22,7 +22,8 @@ from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
-from .kernels.rows import greedy_rows, projection_rows, residual_rows, swiglu_rows
+from .kernels.rows import (greedy_rows, projection_rows, residual_norm_rows, residual_rows,
+                           swiglu_rows)
 from .speculate import draft_width, verified_tokens
 
 
@@ -169,9 +170,12 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
     groups = c.num_attention_heads // c.num_key_value_heads
     rows = b * t
     multi = not c.quantized
+    hn = None  # the down projection's output normalised for the next layer (multi-row path)
     for i, layer in enumerate(model.layers):
         ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
-        if multi:
+        if multi and hn is not None:
+            packed = projection_rows(hn, layer.qkv_weight)
+        elif multi:
             packed = projection_rows(h, layer.qkv_weight, ln1.weight, ln1.variance_epsilon)
         else:
             packed = torch.stack([norm_projection(h[r], ln1.weight, layer.qkv_weight,
@@ -185,7 +189,10 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
         if multi:
             r = residual_rows(a, layer.o_weight, h)
             m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
-            h = residual_rows(m, layer.down_weight, r)
+            nxt = model.layers[i + 1].input_layernorm if i + 1 < len(model.layers) \
+                else model.norm
+            h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,
+                                       nxt.variance_epsilon)
         else:
             r = torch.stack([output_projection_residual(a[j], layer.o_weight, h[j])
                              for j in range(rows)])
@@ -197,8 +204,10 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
     x = h[:, -1:] if last_only else h
     flat = x.reshape(-1, hidden).contiguous()
     if multi:
-        return greedy_rows(flat, model.lm_head_weight, model.norm.weight,
-                           model.norm.variance_epsilon).view(b, x.shape[1])
+        xn = hn.view(b, t, hidden)
+        xn = xn[:, -1:] if last_only else xn
+        return greedy_rows(xn.reshape(-1, hidden).contiguous(),
+                           model.lm_head_weight).view(b, x.shape[1])
     out = torch.empty((flat.shape[0],), dtype=torch.int64, device=model.device)
     for r in range(flat.shape[0]):
         greedy_head(flat[r], model.norm.weight, model.norm.variance_epsilon,

@@ -67,6 +67,31 @@ def residual_rows(x, weight, residual):
     return out
 
 
+def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
+    """(out, normed): out = residual_rows(x, weight, residual) and normed its
+    RMSNorm with `gain` (the next layer's input), finished in one launch when
+    the projection splits K."""
+    _check(x, weight)
+    n = weight.shape[0]
+    if residual.shape != (x.shape[0], n) or residual.dtype != torch.bfloat16 \
+            or residual.stride(1) != 1:
+        raise ValueError("residual must be bf16 [M, N] with unit column stride")
+    if gain is None or gain.shape != (n,) or gain.dtype != torch.bfloat16 \
+            or not gain.is_contiguous():
+        raise ValueError("gain must be a contiguous bf16 [N] vector")
+    _lib.require_gpu(x, weight, residual, gain)
+    out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
+    normed = torch.empty_like(out)
+    for s, e in _chunks(x.shape[0]):
+        rows, k = x[s:e].shape
+        scratch = _scratch(x.device, rows, n, k, _lib.EPI_RESIDUAL, False)
+        _lib.call("htn_gemm_rows_residual_norm", _lib.ptr(x[s:e]), x.stride(0),
+                  _lib.ptr(weight), n, k, rows, _lib.ptr(residual[s:e]), residual.stride(0),
+                  _lib.ptr(out[s:e]), out.stride(0), _lib.ptr(gain), float(eps),
+                  _lib.ptr(normed[s:e]), _lib.ptr(scratch), _lib.stream(x.device))
+    return out, normed
+
+
 def swiglu_rows(x, gate_up_weight, gain=None, eps=1e-6):
     """SwiGLU of the packed gate/up projection ([2I, K]: gate rows, then up rows)."""
     _check(x, gate_up_weight)

@@ -8,8 +8,7 @@ MFMA kernel picks its own K split and sums the fp32 partials in a fixed order.
 """
 import torch
 
-from .rmsnorm import rms_norm
-from .rows import residual_rows
+from .rows import residual_norm_rows, residual_rows
 
 
 def _weight(weight):
@@ -25,5 +24,6 @@ def split_down_residual_norm(x, weight, residual, gain, eps, warps=16):
     """(out, normalized) where normalized is the next layer's RMSNorm input."""
     shape = residual.shape
     rows = x.reshape(-1, x.shape[-1])
-    out = residual_rows(rows, _weight(weight), residual.reshape(-1, shape[-1]))
-    return out.reshape(shape), rms_norm(out, gain, eps).reshape(shape)
+    out, normed = residual_norm_rows(rows, _weight(weight), residual.reshape(-1, shape[-1]),
+                                     gain, eps)
+    return out.reshape(shape), normed.reshape(shape)

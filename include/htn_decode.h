@@ -198,6 +198,21 @@ int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps, 
                   int64_t res_stride, void* y, int64_t y_stride, int64_t* tokens, void* scratch,
                   htn_stream_t stream);
 
+/* The residual projection of htn_gemm_rows (HTN_EPI_RESIDUAL, no input norm)
+ * fused with the next RMSNorm of its output:
+ *   y[m, :]      = bf16(bf16(W x_m) + residual[m, :])      (row stride y_stride)
+ *   normed[m, :] = bf16(gain * bf16(y[m, :] * rsqrt(mean(y[m, :]^2) + eps)))
+ * normed is contiguous [rows, n]. When the projection splits K, the split
+ * finish computes both in one launch; otherwise the projection is followed by
+ * htn_rms_norm. Both paths give the same bits. scratch:
+ * htn_gemm_rows_scratch_bytes(rows, n, k, HTN_EPI_RESIDUAL, 0) bytes.
+ * Replaces the reference's split_down_residual_norm
+ * (dryft/engine/kernels/split_down.py:85-101). */
+int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w, int64_t n,
+                                int64_t k, int64_t rows, const void* residual,
+                                int64_t res_stride, void* y, int64_t y_stride, const void* gain,
+                                float eps, void* normed, void* scratch, htn_stream_t stream);
+
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
                     htn_stream_t stream);

@@ -15,6 +15,7 @@ from hackthenorth_amd import decode as D
 from hackthenorth_amd.kernels import gateup as GU
 from hackthenorth_amd.kernels import projection as P
 from hackthenorth_amd.kernels import rows as RW
+from hackthenorth_amd.kernels.rmsnorm import rms_norm
 from hackthenorth_amd.kernels import split_down as SD
 from hackthenorth_amd.model import Qwen3Model, shape_config
 
@@ -113,6 +114,22 @@ def test_split_down_residual_norm():
     # The strided (transposed-storage) weight the reference accepts.
     out2 = SD.split_down_residual(x.cuda(), w.t().contiguous().t().cuda(), res.cuda())
     torch.testing.assert_close(out2.cpu().float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m,k,n", [(4, 9728, 2560), (20, 9728, 2560), (5, 3072, 1024),
+                                   (4, 12288, 4096)])
+def test_residual_norm_rows_bit_exact(m, k, n):
+    """The fused finish + RMSNorm gives the bits of the residual projection
+    followed by the row-wise RMSNorm (the 9728-deep shapes split K and finish
+    in one launch; the other two have no K split and run both kernels)."""
+    w = nrm(47, (n, k), std=0.02).cuda()
+    x, res, g = nrm(48, (m, k)).cuda(), nrm(49, (m, n)).cuda(), nrm(50, (n,)).cuda()
+    out, normed = RW.residual_norm_rows(x, w, res, g, 1e-6)
+    ref = RW.residual_rows(x, w, res)
+    assert torch.equal(out, ref)
+    assert torch.equal(normed, rms_norm(ref, g, 1e-6))
+    torch.testing.assert_close(out.cpu().float(), Q.output_residual(x.cpu(), w.cpu(), res.cpu()).float(),
+                               atol=2e-2, rtol=2e-2)
 
 
 @pytest.mark.parametrize("length", [2, 5, 8])
