@@ -68,7 +68,7 @@ SIGNATURES = {
     "htn_attention_merge_in_kernel": [],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64}
-EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX, EPI_RESIDUAL_NORM = 0, 1, 2, 3, 4
 
 _lib = None
 _lock = threading.Lock()

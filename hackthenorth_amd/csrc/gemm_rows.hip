@@ -358,6 +358,13 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
   return p;
 }
 
+// The fused residual + RMSNorm keeps the projection's own plan and fuses the
+// norm into its K-split finish when it has one. Splitting K only to get a
+// finish was measured slower (4B verify pass 3.79 -> 3.89 ms, 8B at 4 and 16
+// rows 6-7% slower): the split projection loses more than the norm launch
+// costs, and a 4096-wide row is too long for one wave's finish.
+Plan plan_residual_norm(long M, long N, long K) { return plan(M, N, K, HTN_EPI_RESIDUAL, false); }
+
 }  // namespace
 }  // namespace htn
 
@@ -366,7 +373,8 @@ using namespace htn;
 extern "C" int64_t htn_gemm_rows_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue,
                                                int norm) {
   if (rows <= 0 || rows > kMaxRowsMT || n <= 0 || k <= 0 || k % kStep || k > kMaxK) return 0;
-  const Plan p = plan(rows, n, k, epilogue, norm != 0);
+  const Plan p = epilogue == HTN_EPI_RESIDUAL_NORM ? plan_residual_norm(rows, n, k)
+                                                    : plan(rows, n, k, epilogue, norm != 0);
   return p.norm_bytes + p.tail_bytes;
 }
 
@@ -422,7 +430,8 @@ extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, cons
   if (!x || !w || !residual || !y || !gain || !normed || rows <= 0 || rows > kMaxRowsMT ||
       n <= 0 || k <= 0 || n > (1L << 31))
     return HTN_EINVAL;
-  const Plan p = plan(rows, n, k, HTN_EPI_RESIDUAL, false);
+  if (k % kStep || k > kMaxK) return HTN_EUNSUPPORTED;
+  const Plan p = plan_residual_norm(rows, n, k);
   // One wave holds a row of y in registers: 8-element vectors, at most 8192 columns.
   const bool fused = p.ks > 1 && n % 8 == 0 && n <= 8192 && res_stride % 8 == 0 &&
                      y_stride % 8 == 0 && aligned16(residual) && aligned16(y) &&

@@ -22,8 +22,7 @@ from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
-from .kernels.rows import (greedy_rows, projection_rows, residual_norm_rows, residual_rows,
-                           swiglu_rows)
+from .kernels.rows import greedy_rows, projection_rows, residual_norm_rows, swiglu_rows
 from .speculate import draft_width, verified_tokens
 
 
@@ -187,8 +186,8 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                                   positions)
         a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
         if multi:
-            r = residual_rows(a, layer.o_weight, h)
-            m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
+            r, rn = residual_norm_rows(a, layer.o_weight, h, ln2.weight, ln2.variance_epsilon)
+            m = swiglu_rows(rn, layer.gate_up_weight)
             nxt = model.layers[i + 1].input_layernorm if i + 1 < len(model.layers) \
                 else model.norm
             h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,

@@ -69,8 +69,8 @@ def residual_rows(x, weight, residual):
 
 def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
     """(out, normed): out = residual_rows(x, weight, residual) and normed its
-    RMSNorm with `gain` (the next layer's input), finished in one launch when
-    the projection splits K."""
+    RMSNorm with `gain` (the next layer's input), both written by one launch
+    when the projection splits K."""
     _check(x, weight)
     n = weight.shape[0]
     if residual.shape != (x.shape[0], n) or residual.dtype != torch.bfloat16 \
@@ -84,7 +84,7 @@ def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
     normed = torch.empty_like(out)
     for s, e in _chunks(x.shape[0]):
         rows, k = x[s:e].shape
-        scratch = _scratch(x.device, rows, n, k, _lib.EPI_RESIDUAL, False)
+        scratch = _scratch(x.device, rows, n, k, _lib.EPI_RESIDUAL_NORM, False)
         _lib.call("htn_gemm_rows_residual_norm", _lib.ptr(x[s:e]), x.stride(0),
                   _lib.ptr(weight), n, k, rows, _lib.ptr(residual[s:e]), residual.stride(0),
                   _lib.ptr(out[s:e]), out.stride(0), _lib.ptr(gain), float(eps),

@@ -49,6 +49,7 @@ extern "C" {
 #define HTN_EPI_RESIDUAL 1 /* y = bf16(bf16(dot) + residual) */
 #define HTN_EPI_SWIGLU 2   /* y = bf16(bf16(silu(bf16 gate)) * bf16 up), w holds 2n rows */
 #define HTN_EPI_ARGMAX 3   /* tokens[m] = argmax_n bf16(dot), lowest id on ties */
+#define HTN_EPI_RESIDUAL_NORM 4 /* scratch query of htn_gemm_rows_residual_norm */
 
 typedef void* htn_stream_t;
 
@@ -202,10 +203,12 @@ int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, float eps, 
  * fused with the next RMSNorm of its output:
  *   y[m, :]      = bf16(bf16(W x_m) + residual[m, :])      (row stride y_stride)
  *   normed[m, :] = bf16(gain * bf16(y[m, :] * rsqrt(mean(y[m, :]^2) + eps)))
- * normed is contiguous [rows, n]. When the projection splits K, the split
- * finish computes both in one launch; otherwise the projection is followed by
- * htn_rms_norm. Both paths give the same bits. scratch:
- * htn_gemm_rows_scratch_bytes(rows, n, k, HTN_EPI_RESIDUAL, 0) bytes.
+ * normed is contiguous [rows, n]. When the projection splits K (its plan is
+ * htn_gemm_rows'), the split finish computes both in one launch; otherwise,
+ * and for rows wider than 8192 or unaligned pointers, the projection is
+ * followed by htn_rms_norm. Both paths give the same bits.
+ * scratch: htn_gemm_rows_scratch_bytes(rows, n, k, HTN_EPI_RESIDUAL_NORM, 0)
+ * bytes.
  * Replaces the reference's split_down_residual_norm
  * (dryft/engine/kernels/split_down.py:85-101). */
 int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w, int64_t n,

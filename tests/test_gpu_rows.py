@@ -117,11 +117,11 @@ def test_split_down_residual_norm():
 
 
 @pytest.mark.parametrize("m,k,n", [(4, 9728, 2560), (20, 9728, 2560), (5, 3072, 1024),
-                                   (4, 12288, 4096)])
+                                   (4, 12288, 4096), (5, 4096, 2560)])
 def test_residual_norm_rows_bit_exact(m, k, n):
-    """The fused finish + RMSNorm gives the bits of the residual projection
-    followed by the row-wise RMSNorm (the 9728-deep shapes split K and finish
-    in one launch; the other two have no K split and run both kernels)."""
+    """The fused entry gives the bits of the residual projection followed by
+    the row-wise RMSNorm: the 9728-deep shapes split K and finish both in one
+    launch, the others have no K split and run the two kernels."""
     w = nrm(47, (n, k), std=0.02).cuda()
     x, res, g = nrm(48, (m, k)).cuda(), nrm(49, (m, n)).cuda(), nrm(50, (n,)).cuda()
     out, normed = RW.residual_norm_rows(x, w, res, g, 1e-6)
