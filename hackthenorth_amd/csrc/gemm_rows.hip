@@ -208,62 +208,61 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_finish(RowsArgs a) {
 }
 
 // K-split finish of the residual epilogue fused with the next RMSNorm: one
-// wave per row m. Lane l owns the row's 8-element vectors l, l + 64, ...: it
-// sums their partials in split order, adds the residual, rounds, stores y and
-// keeps the bf16 y vectors in registers; the wave's sum of squares then
-// normalises them. The summation order of the squares (vector by vector,
-// element by element per lane, then one wave reduction) is the row-wise
-// RMSNorm's, so `normed` is bit-identical to running it on y.
-__global__ __launch_bounds__(kWave) void gemm_rows_finish_norm(RowsArgs a) {
-  constexpr int kMaxVec = 16;  // up to 8192 columns
-  const int lane = threadIdx.x;
+// block per row m. Its threads sum the partials of the row's 8-element
+// vectors in split order, add the residual, round, and store y to memory and
+// LDS; wave 0 then forms the sum of squares in the row-wise RMSNorm's order
+// (lane l over vectors l, l + 64, ..., element by element, then one wave
+// reduction), so `normed` is bit-identical to running that norm on y, and
+// every thread normalises its vectors from LDS.
+__global__ __launch_bounds__(kBlock) void gemm_rows_finish_norm(RowsArgs a) {
+  __shared__ uint4 ys[8192 / 8];  // the row of y, up to 8192 columns
+  __shared__ float inv_s;
+  const int tid = threadIdx.x;
   const int m = blockIdx.x;
   const int nv = a.N >> 3;
-  uint4 vals[kMaxVec];
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < kMaxVec; ++j) {
-    const int v = j * 64 + lane;
-    vals[j] = make_uint4(0, 0, 0, 0);
-    if (v < nv) {
-      float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int ks = 0; ks < a.KS; ++ks) {
-        const float4* p =
-            reinterpret_cast<const float4*>(a.part + (static_cast<long>(ks) * a.M + m) * a.N + v * 8);
-        const float4 p0 = p[0], p1 = p[1];
-        t[0] += p0.x; t[1] += p0.y; t[2] += p0.z; t[3] += p0.w;
-        t[4] += p1.x; t[5] += p1.y; t[6] += p1.z; t[7] += p1.w;
-      }
-      float r[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.res + m * a.res_rs + v * 8), r);
-      uint4 yv;
-      yv.x = pack_bf2(round_bf(t[0]) + r[0], round_bf(t[1]) + r[1]);
-      yv.y = pack_bf2(round_bf(t[2]) + r[2], round_bf(t[3]) + r[3]);
-      yv.z = pack_bf2(round_bf(t[4]) + r[4], round_bf(t[5]) + r[5]);
-      yv.w = pack_bf2(round_bf(t[6]) + r[6], round_bf(t[7]) + r[7]);
-      *reinterpret_cast<uint4*>(a.y + m * a.y_rs + v * 8) = yv;
-      vals[j] = yv;
+  for (int v = tid; v < nv; v += kBlock) {
+    float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < a.KS; ++ks) {
+      const float4* p =
+          reinterpret_cast<const float4*>(a.part + (static_cast<long>(ks) * a.M + m) * a.N + v * 8);
+      const float4 p0 = p[0], p1 = p[1];
+      t[0] += p0.x; t[1] += p0.y; t[2] += p0.z; t[3] += p0.w;
+      t[4] += p1.x; t[5] += p1.y; t[6] += p1.z; t[7] += p1.w;
+    }
+    float r[8];
+    unpack8(*reinterpret_cast<const uint4*>(a.res + m * a.res_rs + v * 8), r);
+    uint4 yv;
+    yv.x = pack_bf2(round_bf(t[0]) + r[0], round_bf(t[1]) + r[1]);
+    yv.y = pack_bf2(round_bf(t[2]) + r[2], round_bf(t[3]) + r[3]);
+    yv.z = pack_bf2(round_bf(t[4]) + r[4], round_bf(t[5]) + r[5]);
+    yv.w = pack_bf2(round_bf(t[6]) + r[6], round_bf(t[7]) + r[7]);
+    *reinterpret_cast<uint4*>(a.y + m * a.y_rs + v * 8) = yv;
+    ys[v] = yv;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    float ss = 0.f;
+    for (int v = tid; v < nv; v += kWave) {
       float f[8];
-      unpack8(yv, f);
+      unpack8(ys[v], f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
     }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.N) + a.neps);
+    if (tid == 0) inv_s = inv;
   }
-  const float inv = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.N) + a.neps);
-#pragma unroll
-  for (int j = 0; j < kMaxVec; ++j) {
-    const int v = j * 64 + lane;
-    if (v < nv) {
-      float f[8], g[8];
-      unpack8(vals[j], f);
-      unpack8(*reinterpret_cast<const uint4*>(a.ngain + v * 8), g);
-      uint4 o;
-      o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
-      o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
-      o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
-      o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
-      *reinterpret_cast<uint4*>(a.normed + static_cast<long>(m) * a.N + v * 8) = o;
-    }
+  __syncthreads();
+  const float inv = inv_s;
+  for (int v = tid; v < nv; v += kBlock) {
+    float f[8], g[8];
+    unpack8(ys[v], f);
+    unpack8(*reinterpret_cast<const uint4*>(a.ngain + v * 8), g);
+    uint4 o;
+    o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
+    o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
+    o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
+    o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
+    *reinterpret_cast<uint4*>(a.normed + static_cast<long>(m) * a.N + v * 8) = o;
   }
 }
 
@@ -316,7 +315,7 @@ int launch_w(RowsArgs& a, hipStream_t st) {
   if (EPI == HTN_EPI_ARGMAX) {
     hipLaunchKernelGGL(gemm_rows_argmax, dim3(a.M), dim3(kBlock), 0, st, a.keys, strips, a.M, a.tokens);
   } else if (a.KS > 1 && EPI == HTN_EPI_RESIDUAL && a.normed) {
-    hipLaunchKernelGGL(gemm_rows_finish_norm, dim3(a.M), dim3(kWave), 0, st, a);
+    hipLaunchKernelGGL(gemm_rows_finish_norm, dim3(a.M), dim3(kBlock), 0, st, a);
   } else if (a.KS > 1) {
     const long outs = static_cast<long>(a.M) * a.N;
     hipLaunchKernelGGL((gemm_rows_finish<S, EPI>), dim3((outs + kBlock - 1) / kBlock), dim3(kBlock),
@@ -432,7 +431,7 @@ extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, cons
     return HTN_EINVAL;
   if (k % kStep || k > kMaxK) return HTN_EUNSUPPORTED;
   const Plan p = plan_residual_norm(rows, n, k);
-  // One wave holds a row of y in registers: 8-element vectors, at most 8192 columns.
+  // The finish holds a row of y in LDS: 8-element vectors, at most 8192 columns.
   const bool fused = p.ks > 1 && n % 8 == 0 && n <= 8192 && res_stride % 8 == 0 &&
                      y_stride % 8 == 0 && aligned16(residual) && aligned16(y) &&
                      aligned16(gain) && aligned16(normed);
