@@ -1,34 +1,44 @@
 """Batch-one Qwen3 greedy decode throughput on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-8b]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--headline-only]
 
-Default workload: the Qwen3-0.6B shape (hidden 1024, 28 layers, 16 q / 8 kv
-heads, head_dim 128, FFN 3072, vocab 151936, tied), random-init bf16
-weights N(0, 0.02), a 512-token uniform-random prompt, then K greedy decode
-steps (K = 64: context 512 -> 575). A step is one replay of the captured
-decode graph; the timed region replays K steps back to back with weights,
-KV cache and token/position state already resident in HBM.
+Headline workload: the Qwen3-8B shape (hidden 4096, 36 layers, 32 q / 8 kv
+heads, head_dim 128, FFN 12288, vocab 151936, untied LM head), random-init
+bf16 weights N(0, 0.02), a 2048-token uniform-random prompt, then W untimed
+and K timed greedy decode steps (defaults K = 256, W = 3: context 2048 ->
+2303). A step is one replay of the captured decode graph; the timed region
+replays K steps back to back with weights, KV cache and token/position state
+already resident in HBM. `value` is decode tok/s.
 
-Also reported on the same line:
-  roofline      the dominant kernel (the fused RMSNorm + gate/up GEMV + SwiGLU,
-                one launch per layer), timed alone with HIP events on its stream
-                over rotating per-layer weights (28 x 12.6 MB, more than the
-                256 MB Infinity Cache), as algorithmic bytes / launch time;
-  decode_roofline  bytes per generated token / step time against 8 TB/s;
-  cpu_baseline  the CPU oracle (torch eager, this host's cores) on a bounded
-                sample of the same workload: batched prompt prefill + 8 greedy
-                decode steps, reported as decode tok/s;
-  qwen3_8b      the Qwen3-8B shape (untied), prompt 2048, 256 greedy steps;
+Also on the same line:
+  roofline        the dominant kernel of that step by per-step time (RMSNorm +
+                  gate/up GEMV + SwiGLU, 36 x 31 us of the ~2.9 ms step): launched
+                  back to back in a captured graph over the 36 layers' 201 MB
+                  weights (7.2 GB, far beyond the 256 MB Infinity Cache), timed
+                  with HIP events on the capturing stream; achieved = algorithmic
+                  bytes / average launch; traffic = counted HBM bytes per launch
+                  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes;
+                  also the fraction of a device copy's measured bandwidth;
+  decode_roofline bytes per generated token (every weight once + KV) x tok/s
+                  against 8 TB/s;
+  cpu_baseline    the CPU oracle (torch eager, this host's cores) on a bounded
+                  sample of the same workload: one batched prefill of the 2048-token
+                  prompt, then 8 decode steps fed the GPU's tokens, reported as
+                  decode tok/s, with the teacher-forced parity record of the
+                  GPU's first 9 tokens against the oracle's logits;
+  qwen3_0.6b      the Qwen3-0.6B shape (tied), prompt 512, 64 steps, with its own
+                  dominant kernel (the decode attention at context 512);
+  per_op          the row-wise fused ops at 0.6B widths, 32768 rows and one row;
   qwen3_8b_int8 / qwen3_8b_fp8
-                the Qwen3-8B shape with weight-only int8 / fp8-e4m3fn projections
-                and LM head (uniform integer weights in [-127, 127], per-row
-                scales U(0.001, 0.01)), decoding 128 steps at context 8192 over a
-                synthetic KV cache (N(0,1) keys and values in slots 0..8191);
+                  the 8B shape with weight-only int8 / fp8-e4m3fn projections and
+                  LM head (uniform integer weights in [-127, 127], per-row scales
+                  U(0.001, 0.01)), 128 steps at context 8192 over a synthetic KV
+                  cache (N(0,1) keys and values in slots 0..8191);
   speculative_4b_draft_0.6b
-                Qwen3-4B-shape target with a Qwen3-0.6B-shape draft (both random
-                bf16), k = 4 draft tokens verified in one 5-row pass, context 4096
-                (synthetic KV caches): tok/s, measured greedy acceptance, and the
-                verify pass / draft step / single target step times.
+                  4B-shape target + 0.6B-shape draft (random bf16), k = 4 draft
+                  tokens verified in one 5-row pass, context 4096 (synthetic KV):
+                  tok/s, measured greedy acceptance, verify / step / draft times;
+  batched_qwen3_8b  the 8B shape at batch 4 and 16, context 512.
 """
 import argparse
 import json
@@ -47,20 +57,39 @@ from hackthenorth_amd.kernels import rng as DR  # noqa: E402
 from hackthenorth_amd.model import Qwen3Model, shape_config  # noqa: E402
 
 METRIC = "batch-1 decode tok/s at Qwen3 shapes + per-kernel HBM GB/s as % of peak"
-# HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+# Per-kernel HBM bytes of the 8B decode step, from the committed rocprofv3
 # FETCH_SIZE / WRITE_SIZE passes (calibrated against a copy of known size).
-PMC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gateup_swiglu_qwen3-0.6b_pmc.txt")
+PMC_PROFILE = os.path.join(ROOT, "profiles", "decode_per_kernel_hbm_qwen3-8b.txt")
+TRACE_PROFILE = os.path.join(ROOT, "profiles", "decode_qwen3-8b_bf16_kernel_stats.txt")
 HBM_PEAK_GBS = 8000.0
 PROMPT_SEED, PROMPT_STREAM = 1, 7
+# Greedy-token bar of the parity record (oracle fp32 logit deficit of an
+# emitted token that differs from the oracle's pick); the tests use the same.
+TOKEN_BAR = 2e-2
+DOMINANT_ROLE = "RMSNorm + gate/up GEMV + SwiGLU"
 
 
-def measured_traffic():
+def measured_traffic(role=DOMINANT_ROLE):
+    """Counted HBM bytes per launch (read + write) of a role in the per-kernel table."""
     try:
         with open(PMC_PROFILE) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
-    except OSError:
+                if line.startswith(role + " "):
+                    cols = line[len(role):].split()
+                    return int(round((float(cols[3]) + float(cols[4])) * 1e6))
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def trace_average_us(kernel_prefix):
+    """Average dispatch duration of a kernel in the committed kernel-trace summary."""
+    try:
+        with open(TRACE_PROFILE) as f:
+            for line in f:
+                if line.startswith(kernel_prefix):
+                    return float(line[len(kernel_prefix):].split()[1])
+    except (OSError, ValueError, IndexError):
         pass
     return None
 
@@ -96,8 +125,8 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
         else:
             first = state.prefill(model, prompt.view(1, -1)).clone()
             torch.cuda.synchronize()
-            log(f"{shape}: prefill of {prompt_len} tokens (step by step) "
-                f"{time.perf_counter() - t0:.2f}s")
+            log(f"{shape}: prefill of {prompt_len} tokens {time.perf_counter() - t0:.2f}s")
+        prefill_s = time.perf_counter() - t0
         for _ in range(warmup):
             state.graph.replay()
         # Time exactly `steps` decode steps from the state right after prefill.
@@ -123,6 +152,7 @@ def run_decode(shape, prompt_len, steps, warmup, log, weight_format="bf16",
     tok_s = batch * steps / elapsed
     toks = tokens.cpu()
     return dict(model=model, cfg=cfg, prompt=prompt.cpu().tolist(), first=int(first[0, 0]),
+                prefill_s=prefill_s,
                 tokens=(toks[:, 0] if batch == 1 else toks).tolist(), elapsed=elapsed, tok_s=tok_s,
                 ms_per_step=1e3 * elapsed / steps, bytes_per_token=bytes_per_token,
                 decode_frac=bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9))
@@ -205,44 +235,111 @@ def run_draft_speculation(ctx, steps, k, log):
             "first_tokens": tokens[:8]}
 
 
-def dominant_kernel(model, launches=280):
-    """Fused norm + gate/up + SwiGLU GEMV over the layers' weights (one launch per
-    layer, rotating through all of them), captured in a graph so the launches run
-    back to back, timed with HIP events on the capturing stream."""
-    cfg = model.config
-    layers = model.layers
-    x = torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16, device=model.device)
-    DR.normal_(x, 3, 99, 1.0)
-    gain = layers[0].post_attention_layernorm.weight
-    stream = torch.cuda.Stream(device=model.device)
-    stream.wait_stream(torch.cuda.current_stream())
+def graph_launch_us(calls, device, replays=1):
+    """Average duration of one launch of `calls` (callables, each one kernel
+    launch sequence) captured back to back in a graph, timed with HIP events
+    recorded on the capturing stream around the replay."""
+    stream = torch.cuda.Stream(device=device)
+    stream.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(stream):
-        for layer in layers[:4]:
-            P.norm_projection(x, gain, layer.gate_up_weight, 1e-6, swiglu=True)
-    torch.cuda.current_stream().wait_stream(stream)
+        for fn in calls[:4]:
+            fn()
+    torch.cuda.current_stream(device).wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for i in range(launches):
-            P.norm_projection(x, gain, layers[i % len(layers)].gate_up_weight, 1e-6, swiglu=True)
-    graph.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.inference_mode(), torch.cuda.graph(graph, stream=stream):
+        for fn in calls:
+            fn()
     with torch.cuda.stream(stream):
-        start.record(stream)
         graph.replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
         end.record(stream)
     end.synchronize()
-    avg_s = start.elapsed_time(end) / 1e3 / launches
+    return start.elapsed_time(end) * 1e3 / (replays * len(calls))
+
+
+def dominant_kernel(model, rounds=4):
+    """Fused RMSNorm + gate/up GEMV + SwiGLU, one launch per layer, rotating
+    through all layers' weights `rounds` times, back to back in a graph."""
+    cfg = model.config
+    layers = model.layers
+    x = DR.normal_(torch.empty((1, 1, cfg.hidden_size), dtype=torch.bfloat16,
+                               device=model.device), 3, 99, 1.0)
+    gain = layers[0].post_attention_layernorm.weight
+    calls = [(lambda w=layers[i % len(layers)].gate_up_weight:
+              P.norm_projection(x, gain, w, 1e-6, swiglu=True))
+             for i in range(rounds * len(layers))]
+    avg_us = graph_launch_us(calls, model.device)
     k, n2 = cfg.hidden_size, 2 * cfg.intermediate_size
     algorithmic = n2 * k * 2 + k * 2 * 2 + cfg.intermediate_size * 2  # W + x + gain + y
-    achieved = algorithmic / avg_s / 1e9
     return dict(name="gemv_vec<norm, swiglu> (RMSNorm + gate/up GEMV + SwiGLU)",
-                avg_us=avg_s * 1e6, bytes=algorithmic, achieved=achieved)
+                instance="void htn::gemv_vec<1, 2, 8, true, 2, 0>(htn::GemvArgs)",
+                avg_us=avg_us, bytes=algorithmic, achieved=algorithmic / avg_us / 1e3,
+                launches=len(calls), weights_rotated_bytes=len(layers) * n2 * k * 2)
 
 
-def per_op_microbench(reps=10):
-    """Bandwidth of the row-wise fused ops at Qwen3-0.6B widths over 32768 rows
-    (bf16 activations N(0,1)): algorithmic bytes / average launch time."""
+def attention_kernel(model, ctx, rounds=4):
+    """The decode step's attention launch (QK-norm + RoPE + KV append +
+    split-KV GQA attention + merge, with the O-weight prefetch of the step) at
+    position `ctx`, one launch per layer over every layer's cache, back to back
+    in a graph. Algorithmic bytes: the K/V rows of slots 0..ctx, the packed
+    q/k/v row in, the attention row out, the RoPE row and the two gains."""
+    from hackthenorth_amd.kernels.attention import prologue_attention
+    cfg = model.config
+    c = cfg
+    cap = ctx + 1
+    dev = model.device
+    cache = D.KVCache(model, 1, cap)
+    DR.normal_(cache.storage.view(-1), 21, 79, 1.0)
+    rotary = D.RotaryTable(model, cap)
+    position = torch.tensor([ctx], dtype=torch.int64, device=dev)
+    rope = rotary.step_row(position)
+    q_width, k_width, _ = c.widths
+    packed = DR.normal_(torch.empty((1, 1, sum(c.widths)), dtype=torch.bfloat16, device=dev),
+                        5, 98, 1.0)
+    groups = c.num_attention_heads // c.num_key_value_heads
+    layers = model.layers
+    calls = [(lambda i=i % len(layers): prologue_attention(
+        packed, layers[i].q_norm, layers[i].k_norm, rope[0], rope[1], cache.keys[i],
+        cache.values[i], position, c.num_key_value_heads, groups, q_width, q_width + k_width,
+        next_weight=layers[i].o_weight)) for i in range(rounds * len(layers))]
+    avg_us = graph_launch_us(calls, dev)
+    kv = 2 * c.num_key_value_heads * (ctx + 1) * c.head_dim * 2
+    io = sum(c.widths) * 2 + q_width * 2 + 2 * c.head_dim * 2 + 2 * c.head_dim * 2
+    algorithmic = kv + io
+    del cache
+    return dict(name="prologue attention (QK-norm + RoPE + KV append + split-KV GQA + merge)",
+                avg_us=avg_us, bytes=algorithmic, achieved=algorithmic / avg_us / 1e3,
+                context=ctx, launches=len(calls))
+
+
+def copy_peak(nbytes=2 << 30, reps=5):
+    """Device-to-device copy bandwidth (bytes read + written per second, GB/s)."""
+    src = DR.normal_(torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda"), 9, 9, 1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / reps
+    del src, dst
+    return 2 * nbytes / sec / 1e9
+
+
+def per_op_microbench(reps=10, latency_launches=200):
+    """The row-wise fused ops at Qwen3-0.6B widths (bf16 activations N(0,1)):
+    bandwidth over 32768 rows (algorithmic bytes / average launch time; the
+    inputs are re-read every repetition, and 0.3-0.6 GB working sets exceed the
+    256 MB Infinity Cache), and the batch-one latency of one row (the decode
+    step's case) as the average of `latency_launches` back-to-back launches in
+    a graph."""
     from hackthenorth_amd.kernels import embed as E
     from hackthenorth_amd.kernels import fused as F
     from hackthenorth_amd.kernels import rmsnorm as N
@@ -265,14 +362,19 @@ def per_op_microbench(reps=10):
         end.synchronize()
         return start.elapsed_time(end) / 1e3 / reps
 
+    def one_row_us(fn):
+        return graph_launch_us([fn] * latency_launches, dev)
+
     out = {}
     x, r, g = randn((rows, H), 1), randn((rows, H), 2), randn((H,), 3)
     t = timed(lambda: N.add_rms_norm(x, r, g, 1e-6))
-    out["add_rms_norm"] = (rows * H * 2 * 4 + H * 2, t, f"[{rows}, {H}]")
+    t1 = one_row_us(lambda: N.add_rms_norm(x[:1], r[:1], g, 1e-6))
+    out["add_rms_norm"] = (rows * H * 2 * 4 + H * 2, t, f"[{rows}, {H}]", t1)
     del x, r
     gate, up = randn((rows, I), 4), randn((rows, I), 5)
     t = timed(lambda: F.swiglu(gate, up))
-    out["swiglu"] = (rows * I * 2 * 3, t, f"[{rows}, {I}]")
+    t1 = one_row_us(lambda: F.swiglu(gate[:1], up[:1]))
+    out["swiglu"] = (rows * I * 2 * 3, t, f"[{rows}, {I}]", t1)
     del gate, up
     packed = randn((1, rows, (Hq + 2 * Hkv) * Dh), 6)
     q, k, v = (u.view(1, rows, -1, Dh) for u in packed.split((Hq * Dh, Hkv * Dh, Hkv * Dh), -1))
@@ -282,52 +384,77 @@ def per_op_microbench(reps=10):
     values = torch.zeros_like(keys)
     positions = torch.arange(rows, device=dev)
     t = timed(lambda: F.norm_rope_cache(q, k, v, qn, kn, cos, sin, keys, values, positions))
+    t1 = one_row_us(lambda: F.norm_rope_cache(q[:, :1], k[:, :1], v[:, :1], qn, kn, cos[:, :1],
+                                              sin[:, :1], keys, values, positions[:1]))
     per_token = (Hq + 2 * Hkv) * Dh * 2 * 2 + 2 * Dh * 2 + 8
-    out["qk_norm_rope_kv_append"] = (rows * per_token, t, f"{rows} tokens x ({Hq} q + {Hkv} kv heads)")
+    out["qk_norm_rope_kv_append"] = (rows * per_token, t,
+                                     f"{rows} tokens x ({Hq} q + {Hkv} kv heads)", t1)
     del packed, keys, values
     table = randn((V, H), 9)
     ids = DR.randint(rows, V, 1, 8, device=dev)
     t = timed(lambda: E.embed_gather(ids, table))
-    out["embed_gather"] = (rows * (H * 2 * 2 + 8), t, f"{rows} ids of [{V}, {H}]")
+    t1 = one_row_us(lambda: E.embed_gather(ids[:1], table))
+    out["embed_gather"] = (rows * (H * 2 * 2 + 8), t, f"{rows} ids of [{V}, {H}]", t1)
     return {name: {"shape": shape, "bytes": b, "us": round(sec * 1e6, 2),
-                   "GBs": round(b / sec / 1e9, 1), "frac_of_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
-            for name, (b, sec, shape) in out.items()}
+                   "GBs": round(b / sec / 1e9, 1),
+                   "frac_of_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4),
+                   "one_row_us": round(t1, 3)}
+            for name, (b, sec, shape, t1) in out.items()}
 
 
-def cpu_baseline(prompt, steps_gpu_tokens, first_gpu, decode_steps=8):
+def oracle_weights(model):
+    """The device model's weights as the oracle's CPU dictionary (bit-identical
+    to oracle.qwen3.generate_weights for the same seed, which the GPU tests
+    check; copying them is far faster than regenerating 8B weights in numpy)."""
+    w = {"embed": model.embed_weight.cpu(), "norm": model.norm.weight.cpu()}
+    w["lm_head"] = (w["embed"] if model.lm_head_weight is model.embed_weight
+                    else model.lm_head_weight.cpu())
+    for i, layer in enumerate(model.layers):
+        for kind, t in layer.tensors().items():
+            w[f"{i}.{kind}"] = t.cpu()
+        w[f"{i}.ln1"] = layer.input_layernorm.weight.cpu()
+        w[f"{i}.ln2"] = layer.post_attention_layernorm.weight.cpu()
+        w[f"{i}.q_norm"] = layer.q_norm.weight.cpu()
+        w[f"{i}.k_norm"] = layer.k_norm.weight.cpu()
+    return w
+
+
+def cpu_baseline(model, shape_name, prompt, gpu_tokens, decode_steps=8):
+    """The CPU oracle on this host's cores over a bounded sample of the
+    workload: one batched prefill of the whole prompt, then `decode_steps`
+    decode steps fed the GPU's own tokens (teacher forcing), which also gives
+    the parity record of those tokens against the oracle's logits."""
+    from oracle import parity as OP
     from oracle import qwen3 as Q
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
-    shape = Q.SHAPES["0.6b"]
-    weights = Q.generate_weights(shape, seed=0)
+    shape = Q.SHAPES[shape_name]
+    t0 = time.perf_counter()
+    weights = oracle_weights(model)
     oracle = Q.Oracle(shape, weights, capacity=len(prompt) + decode_steps + 1)
-    cache = Q.new_cache(shape, oracle.capacity)
-    ids = torch.tensor([prompt], dtype=torch.int64)
-    t0 = time.perf_counter()
-    tok, _, _ = oracle.forward(ids, cache, torch.arange(len(prompt)))
-    prefill_s = time.perf_counter() - t0
-    tokens = [int(tok[0, 0])]
-    t0 = time.perf_counter()
-    for i in range(decode_steps):
-        pos = torch.tensor([len(prompt) + i])
-        tok, _, _ = oracle.forward(torch.tensor([[tokens[-1]]]), cache, pos)
-        tokens.append(int(tok[0, 0]))
-    decode_s = time.perf_counter() - t0
-    agree = tokens[0] == first_gpu and tokens[1:] == steps_gpu_tokens[:decode_steps]
+    setup_s = time.perf_counter() - t0
+    timer = {}
+    record = OP.teacher_forced(oracle, prompt, gpu_tokens[:decode_steps + 1], TOKEN_BAR,
+                               timer=timer)
+    del oracle, weights
     cpu_name = ""
     try:
         with open("/proc/cpuinfo") as f:
             cpu_name = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except (OSError, StopIteration):
         pass
-    return {"value": decode_steps / decode_s, "unit": "tok/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"CPU oracle (torch eager, bf16 rounding of the reference path) on the same "
-                      f"0.6B workload: one batched prefill of the {len(prompt)}-token prompt "
-                      f"({prefill_s:.1f}s) then {decode_steps} greedy decode steps at ctx "
-                      f"{len(prompt)}-{len(prompt) + decode_steps - 1}; tok/s over the decode steps",
-            "prefill_s": round(prefill_s, 3), "tokens_match_gpu": bool(agree),
-            "cpu_tokens": tokens, "gpu_tokens": [first_gpu] + list(steps_gpu_tokens[:decode_steps]),
+    return {"value": decode_steps / timer["decode_s"], "unit": "tok/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"CPU oracle (torch eager, fp32 accumulation with the reference's bf16 "
+                      f"rounding boundaries) on the same {shape_name} workload and weights: one "
+                      f"batched prefill of the {len(prompt)}-token prompt "
+                      f"({timer['prefill_s']:.1f} s) then {decode_steps} decode steps at context "
+                      f"{len(prompt)}-{len(prompt) + decode_steps - 1} fed the GPU's tokens; "
+                      f"value = tok/s over those decode steps",
+            "prefill_s": round(timer["prefill_s"], 3),
+            "prefill_tok_s": round(len(prompt) / timer["prefill_s"], 1),
+            "decode_s": round(timer["decode_s"], 3), "setup_s": round(setup_s, 1),
+            "teacher_forced": record.summary(),
             "cpu_model": cpu_name, "os_cpu_count": os.cpu_count(),
             "affinity_cpus": len(os.sched_getaffinity(0))}
 
@@ -369,21 +496,50 @@ def pmc_pass(shape="qwen3-0.6b"):
           flush=True)
 
 
+def decode_line(res):
+    """The common keys of a decode result."""
+    return {"tok_s": round(res["tok_s"], 2), "ms_per_step": round(res["ms_per_step"], 4),
+            "bytes_per_token": res["bytes_per_token"],
+            "roofline_frac": round(res["decode_frac"], 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / res["bytes_per_token"], 1)}
+
+
+def section_0p6b(args, log):
+    """The Qwen3-0.6B decode (prompt 512, 64 steps) with its dominant kernel:
+    the decode attention (28 x ~7.7 us per step against 28 x ~5 us for the
+    gate/up GEMV in the step's kernel trace)."""
+    r = run_decode("qwen3-0.6b", 512, 64, args.warmup, log)
+    att = attention_kernel(r["model"], 512)
+    log(f"qwen3-0.6b: {r['tok_s']:.1f} tok/s; attention {att['avg_us']:.2f} us/launch")
+    out = {"workload": "Qwen3-0.6B-shape bf16 (tied), prompt 512, 64 greedy steps "
+                       "(context 512-575)", **decode_line(r),
+           "dominant_kernel": {"kernel": att["name"], "avg_launch_us": round(att["avg_us"], 3),
+                               "bytes_per_launch": att["bytes"], "context": att["context"],
+                               "achieved_GBs": round(att["achieved"], 1),
+                               "frac": round(att["achieved"] / HBM_PEAK_GBS, 4)},
+           "first_tokens": [r["first"]] + r["tokens"][:15]}
+    del r
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-8b", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="the 8B headline line only (no secondary sections, no CPU baseline)")
+    ap.add_argument("--cpu-decode-steps", type=int, default=8)
     ap.add_argument("--quiet", action="store_true")
-    ap.add_argument("--pmc-shape", default="qwen3-0.6b", choices=("qwen3-0.6b", "qwen3-8b"),
+    ap.add_argument("--pmc-shape", default="qwen3-8b", choices=("qwen3-0.6b", "qwen3-8b"),
                     help="model shape of the --pmc-pass workload")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
-                    choices=("all", "qwen3-8b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
+                    choices=("all", "qwen3-0.6b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
                              "batched", "per-op"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -404,9 +560,8 @@ def main():
             print(msg, file=sys.stderr, flush=True)
 
     if args.section != "all":
-        if args.section == "qwen3-8b":
-            r = run_decode("qwen3-8b", 2048, 256, args.warmup, log)
-            out = {k: r[k] for k in ("tok_s", "ms_per_step", "bytes_per_token", "decode_frac")}
+        if args.section == "qwen3-0.6b":
+            out = section_0p6b(args, log)
         elif args.section == "speculative":
             out = run_draft_speculation(4096, 128, 4, log)
         elif args.section == "batched":
@@ -417,85 +572,88 @@ def main():
             fmt = "int8" if args.section.endswith("int8") else "fp8_e4m3"
             r = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
                            synthetic_context=True)
-            out = {k: r[k] for k in ("tok_s", "ms_per_step", "bytes_per_token", "decode_frac")}
+            out = decode_line(r)
         print(json.dumps({"section": args.section, **out}), flush=True)
         return
 
-    res = run_decode("qwen3-0.6b", args.prompt, args.steps, args.warmup, log)
-    log(f"qwen3-0.6b: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step")
+    # Headline: Qwen3-8B shape, bf16, prompt 2048, K timed greedy steps.
+    res = run_decode("qwen3-8b", args.prompt, args.steps, args.warmup, log)
+    log(f"qwen3-8b: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step "
+        f"({100 * res['decode_frac']:.1f}% of the bytes roofline)")
     dom = dominant_kernel(res["model"])
     log(f"dominant kernel: {dom['avg_us']:.2f} us/launch, {dom['achieved']:.0f} GB/s")
+    copy_gbs = copy_peak()
+    log(f"device copy: {copy_gbs:.0f} GB/s")
+    trace_us = trace_average_us(dom["instance"])
     line = {
         "metric": METRIC, "value": round(res["tok_s"], 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: random-init N(0,0.02) bf16 weights and uniform prompt ids from the "
                 "counter RNG (seed 0 weights, seed 1 prompt)",
-        "config": {"workload": "Qwen3-0.6B-shape bf16 batch-1 greedy decode, prompt "
-                               f"{args.prompt}, {args.steps} steps (context {args.prompt}-"
-                               f"{args.prompt + args.steps - 1}), captured HIP graph per step",
+        "config": {"workload": f"Qwen3-8B-shape bf16 batch-1 greedy decode (hidden 4096, 36 "
+                               f"layers, 32 q / 8 kv heads, FFN 12288, vocab 151936, untied), "
+                               f"prompt {args.prompt}, {args.steps} timed steps (context "
+                               f"{args.prompt}-{args.prompt + args.steps - 1}), one captured "
+                               f"HIP graph per step",
                    "batch": 1, "prompt_tokens": args.prompt, "decode_steps": args.steps},
         "roofline": {"bound": "hbm", "achieved": round(dom["achieved"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": dom["name"], "avg_launch_us": round(dom["avg_us"], 3),
-                     "bytes_per_launch": dom["bytes"]},
+                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": dom["name"], "instance": dom["instance"],
+                     "avg_launch_us": round(dom["avg_us"], 3),
+                     "bytes_per_launch": dom["bytes"], "launches_timed": dom["launches"],
+                     "weights_rotated_bytes": dom["weights_rotated_bytes"],
+                     "trace_avg_us": trace_us,
+                     "trace_frac": (round(dom["bytes"] / trace_us / 1e3 / HBM_PEAK_GBS, 4)
+                                    if trace_us else None),
+                     "copy_peak_GBs": round(copy_gbs, 1),
+                     "frac_of_copy_peak": round(dom["achieved"] / copy_gbs, 4)},
         "decode_roofline": {"bytes_per_token": res["bytes_per_token"],
                             "achieved_GBs": round(res["bytes_per_token"] * res["tok_s"] / 1e9, 1),
                             "frac": round(res["decode_frac"], 4),
+                            "frac_of_copy_peak": round(
+                                res["bytes_per_token"] * res["tok_s"] / 1e9 / copy_gbs, 4),
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / res["bytes_per_token"], 1)},
+        "prefill_s": round(res["prefill_s"], 3),
         "first_tokens": [res["first"]] + res["tokens"][:15],
     }
+    if not args.no_cpu_baseline and not args.headline_only:
+        try:
+            line["cpu_baseline"] = cpu_baseline(res["model"], "8b", res["prompt"],
+                                                [res["first"]] + res["tokens"],
+                                                args.cpu_decode_steps)
+            tf = line["cpu_baseline"]["teacher_forced"]
+            log(f"cpu baseline: {line['cpu_baseline']['value']:.2f} tok/s decode, prefill "
+                f"{line['cpu_baseline']['prefill_s']:.1f} s; teacher-forced "
+                f"{tf['identical']}/{tf['checked']} identical, max deficit {tf['max_deficit']:.4g}")
+        except Exception as exc:  # report, do not lose the headline line
+            line["cpu_baseline"] = {"error": repr(exc)}
     del res["model"]
     torch.cuda.empty_cache()
-    line["per_op"] = per_op_microbench()
-    torch.cuda.empty_cache()
-    if not args.no_8b:
-        try:
-            r8 = run_decode("qwen3-8b", 2048, 256, args.warmup, log)
-            del r8["model"]
-            torch.cuda.empty_cache()
-            line["qwen3_8b"] = {"workload": "Qwen3-8B-shape bf16, prompt 2048, 256 greedy steps",
-                                "tok_s": round(r8["tok_s"], 2),
-                                "ms_per_step": round(r8["ms_per_step"], 4),
-                                "bytes_per_token": r8["bytes_per_token"],
-                                "roofline_frac": round(r8["decode_frac"], 4),
-                                "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r8["bytes_per_token"], 1)}
-            log(f"qwen3-8b: {r8['tok_s']:.1f} tok/s ({100 * r8['decode_frac']:.1f}% of roofline)")
-        except Exception as exc:  # report, do not lose the headline line
-            line["qwen3_8b"] = {"error": repr(exc)}
+    if not args.headline_only:
+        sections = [("qwen3_0.6b", lambda: section_0p6b(args, log)),
+                    ("per_op", per_op_microbench)]
         for fmt in ("int8", "fp8_e4m3"):
-            key = "qwen3_8b_" + fmt.split("_")[0]
+            sections.append((f"qwen3_8b_{fmt.split('_')[0]}",
+                             lambda fmt=fmt: {"workload": f"Qwen3-8B-shape, weight-only {fmt} "
+                                              "projections and LM head, bf16 activations and KV, "
+                                              "128 greedy steps at context 8192-8319 (synthetic "
+                                              "N(0,1) KV cache)",
+                                              **decode_line(run_decode(
+                                                  "qwen3-8b", 8192, 128, args.warmup, log,
+                                                  weight_format=fmt, synthetic_context=True))}))
+        sections.append(("speculative_4b_draft_0.6b",
+                         lambda: run_draft_speculation(4096, 128, 4, log)))
+        sections.append(("batched_qwen3_8b",
+                         lambda: run_batched("qwen3-8b", 512, 32, (4, 16), log)))
+        for key, fn in sections:
             try:
-                rq = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
-                                synthetic_context=True)
-                del rq["model"]
-                torch.cuda.empty_cache()
-                line[key] = {"workload": f"Qwen3-8B-shape, weight-only {fmt} projections and LM "
-                                         "head, bf16 activations and KV, 128 greedy steps at "
-                                         "context 8192-8319 (synthetic N(0,1) KV cache)",
-                             "tok_s": round(rq["tok_s"], 2),
-                             "ms_per_step": round(rq["ms_per_step"], 4),
-                             "bytes_per_token": rq["bytes_per_token"],
-                             "roofline_frac": round(rq["decode_frac"], 4),
-                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / rq["bytes_per_token"], 1)}
-                log(f"qwen3-8b {fmt}: {rq['tok_s']:.1f} tok/s "
-                    f"({100 * rq['decode_frac']:.1f}% of roofline)")
-            except Exception as exc:
+                line[key] = fn()
+            except Exception as exc:  # report, do not lose the headline line
                 line[key] = {"error": repr(exc)}
-    if not args.no_8b:
-        try:
-            line["speculative_4b_draft_0.6b"] = run_draft_speculation(4096, 128, 4, log)
-        except Exception as exc:
-            line["speculative_4b_draft_0.6b"] = {"error": repr(exc)}
-        torch.cuda.empty_cache()
-        try:
-            line["batched_qwen3_8b"] = run_batched("qwen3-8b", 512, 32, (4, 16), log)
-        except Exception as exc:
-            line["batched_qwen3_8b"] = {"error": repr(exc)}
-        torch.cuda.empty_cache()
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(res["prompt"], res["tokens"], res["first"])
+            torch.cuda.empty_cache()
     print(json.dumps(line), flush=True)
 
 

@@ -154,10 +154,12 @@ def _attention_chunks(q, keys, values, positions, groups):
     return out.view(b * t, heads * dim)
 
 
-def _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings, rotary):
+def _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings, rotary,
+                  record=None):
     """Any batch and token count (prefill, verify): multi-row MFMA projections
     that read each weight once per 32 rows, batched norm/RoPE/cache append and
-    grouped attention. 8-bit weights take the batch-one GEMVs row by row."""
+    grouped attention. 8-bit weights take the batch-one GEMVs row by row.
+    `record`, when a list, receives every layer's output rows [B, T, H]."""
     c = model.config
     b, t = token_ids.shape
     hidden = c.hidden_size
@@ -199,19 +201,22 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                                              ln2.variance_epsilon, swiglu=True)
                              for j in range(rows)])
             h = torch.stack([down_residual(m[j], layer.down_weight, r[j]) for j in range(rows)])
-    h = h.view(b, t, hidden)
-    x = h[:, -1:] if last_only else h
-    flat = x.reshape(-1, hidden).contiguous()
+        if record is not None:
+            record.append(h.view(b, t, hidden))
+    kept = 1 if last_only else t
     if multi:
+        # hn is the final RMSNorm of h (the last down projection fused it).
         xn = hn.view(b, t, hidden)
         xn = xn[:, -1:] if last_only else xn
         return greedy_rows(xn.reshape(-1, hidden).contiguous(),
-                           model.lm_head_weight).view(b, x.shape[1])
+                           model.lm_head_weight).view(b, kept)
+    x = h.view(b, t, hidden)
+    flat = (x[:, -1:] if last_only else x).reshape(-1, hidden).contiguous()
     out = torch.empty((flat.shape[0],), dtype=torch.int64, device=model.device)
     for r in range(flat.shape[0]):
         greedy_head(flat[r], model.norm.weight, model.norm.variance_epsilon,
                     model.lm_head_weight, out[r:r + 1])
-    return out.view(b, x.shape[1])
+    return out.view(b, kept)
 
 
 def forward(model, token_ids, cache, positions, attention_mask=None, last_only=True,
@@ -223,8 +228,8 @@ def forward(model, token_ids, cache, positions, attention_mask=None, last_only=T
     ignored, as in the reference's position-causal attention. K/V of the new
     tokens are written to cache slots `positions`. With a RotaryTable and a
     single token at batch one the fused step runs; `out`/`advance` then
-    receive the token and a position increment in place, and `record` (a
-    list) collects the per-layer hidden states.
+    receive the token and a position increment in place. `record` (a list)
+    collects the per-layer hidden states on either path.
     """
     b, t = token_ids.shape
     if b == 1 and t == 1 and rotary is not None and position_embeddings is None:
@@ -232,7 +237,7 @@ def forward(model, token_ids, cache, positions, attention_mask=None, last_only=T
     if rotary is None and position_embeddings is None:
         rotary = RotaryTable(model, cache.capacity)
     tokens = _forward_rows(model, token_ids, cache, positions, last_only, position_embeddings,
-                           rotary)
+                           rotary, record)
     if out is not None:
         out.copy_(tokens[:, -1:])
     if advance is not None:
@@ -280,7 +285,11 @@ class DecodeState:
         prompt_length = self.shape[1]
         stream = torch.cuda.Stream(device=model.device)
         stream.wait_stream(torch.cuda.current_stream(model.device))
-        with torch.cuda.stream(stream):
+        # Captures always run in inference mode: torch keeps per-generator
+        # graph state tensors shared by every live graph, created in the mode
+        # of the capture that made them; capturing in inference mode can
+        # update them whichever mode made them.
+        with torch.inference_mode(), torch.cuda.stream(stream):
             # Library load and allocator warm-up happen off capture.
             for _ in range(2):
                 self.position.fill_(prompt_length)
@@ -288,7 +297,7 @@ class DecodeState:
             self.position.fill_(prompt_length)
         torch.cuda.current_stream(model.device).wait_stream(stream)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=stream):
+        with torch.inference_mode(), torch.cuda.graph(self.graph, stream=stream):
             self.step(model)
 
     def prefill(self, model, input_ids):
@@ -334,12 +343,12 @@ class DecodeState:
         self.position.fill_(prompt_length)
         stream = torch.cuda.Stream(device=device)
         stream.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(stream):
+        with torch.inference_mode(), torch.cuda.stream(stream):
             for _ in range(2):
                 self.verify_step(model)
         torch.cuda.current_stream(device).wait_stream(stream)
         self.verify_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.verify_graph, stream=stream):
+        with torch.inference_mode(), torch.cuda.graph(self.verify_graph, stream=stream):
             self.verify_output = self.verify_step(model)
         self.position.fill_(prompt_length)
 

@@ -44,14 +44,15 @@ class DraftSpeculator:
         self.proposal = torch.zeros((self.k,), dtype=torch.int64, device=device)
         stream = torch.cuda.Stream(device=device)
         stream.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(stream):
+        # In inference mode, as DecodeState.capture (torch's shared graph RNG state).
+        with torch.inference_mode(), torch.cuda.stream(stream):
             ds.position.fill_(self.shape[1])
             for i in range(self.k):
                 ds.step(self.draft)
                 self.proposal[i:i + 1].copy_(ds.token[0])
         torch.cuda.current_stream(device).wait_stream(stream)
         self.draft_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.draft_graph, stream=stream):
+        with torch.inference_mode(), torch.cuda.graph(self.draft_graph, stream=stream):
             for i in range(self.k):
                 ds.step(self.draft)
                 self.proposal[i:i + 1].copy_(ds.token[0])

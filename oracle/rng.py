@@ -27,6 +27,8 @@ limits, and hand-computed splitmix64 values for known counters; the e4m3fn
 encoder and decoder are checked against torch.float8_e4m3fn conversions over
 every code and over all integers in [-127, 127].
 """
+import os
+
 import numpy as np
 
 GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -97,11 +99,27 @@ def normal_f32(seed, stream, count, std=1.0, start=0):
     return out
 
 
+def _chunked(count, fill):
+    """Run fill(lo, n) over CHUNK-sized pieces on a thread pool (numpy releases
+    the GIL in its array loops); each piece writes its own output range."""
+    pieces = [(lo, min(CHUNK, count - lo)) for lo in range(0, count, CHUNK)]
+    if len(pieces) <= 1:
+        for lo, n in pieces:
+            fill(lo, n)
+        return
+    from concurrent.futures import ThreadPoolExecutor
+    workers = min(16, len(pieces), len(os.sched_getaffinity(0)))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(lambda p: fill(*p), pieces))
+
+
 def normal_bf16_bits(seed, stream, count, std=1.0, start=0):
     out = np.empty(count, dtype=np.uint16)
-    for lo in range(0, count, CHUNK):
-        n = min(CHUNK, count - lo)
+
+    def fill(lo, n):
         out[lo:lo + n] = f32_to_bf16_bits(normal_f32(seed, stream, n, std, start + lo))
+
+    _chunked(count, fill)
     return out
 
 
@@ -120,10 +138,16 @@ def uniform_f32(seed, stream, count, low, high, start=0):
 
 def int8_uniform(seed, stream, count, start=0):
     """Uniform int8 in [-127, 127]."""
-    h = hashes(seed, stream, start, count)
-    with np.errstate(over="ignore"):
-        v = ((h >> np.uint64(32)) * np.uint64(255)) >> np.uint64(32)
-    return (v.astype(np.int64) - 127).astype(np.int8)
+    out = np.empty(count, dtype=np.int8)
+
+    def fill(lo, n):
+        h = hashes(seed, stream, start + lo, n)
+        with np.errstate(over="ignore"):
+            v = ((h >> np.uint64(32)) * np.uint64(255)) >> np.uint64(32)
+        out[lo:lo + n] = (v.astype(np.int64) - 127).astype(np.int8)
+
+    _chunked(count, fill)
+    return out
 
 
 def int8_codes(seed, stream, count, start=0):
@@ -169,7 +193,9 @@ def w8_codes(seed, stream, count, fmt, start=0):
     if fmt == "int8":
         return v.view(np.uint8)
     if fmt == "fp8_e4m3":
-        return e4m3_encode(v.astype(np.float32))
+        # e4m3_encode of each of the 255 possible integers, looked up per weight.
+        table = e4m3_encode(np.arange(-127, 128, dtype=np.float32))
+        return table[v.astype(np.int64) + 127]
     raise ValueError(fmt)
 
 
@@ -177,4 +203,5 @@ def w8_values(codes, fmt):
     """Exact float32 values of 8-bit weight codes."""
     if fmt == "int8":
         return np.asarray(codes, dtype=np.uint8).view(np.int8).astype(np.float32)
-    return e4m3_decode(codes)
+    # e4m3_decode of each of the 256 codes, looked up per weight.
+    return e4m3_decode(np.arange(256, dtype=np.uint8))[np.asarray(codes, dtype=np.uint8)]

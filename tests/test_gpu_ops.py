@@ -404,7 +404,7 @@ def test_captured_graph_replays_track_changed_inputs():
     run()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.inference_mode(), torch.cuda.graph(graph):
         out = run()
     for step in range(6):
         x.copy_(cuda(nrm(80 + step, (1, 1, k))))
