@@ -38,6 +38,7 @@ constexpr int kCounterStride = 32;  // uint32 words
 constexpr int kMaxCounterPairs = 256;
 constexpr long kCounterBytes = static_cast<long>(kMaxCounterPairs) * kCounterStride * 4;
 static_assert(kCounterBytes == HTN_ATTENTION_COUNTER_BYTES, "counter region size");
+static_assert(kMaxQ == 8, "load_pos8 reads eight positions");
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
 //   n = bf16(g * bf16(x * inv)); out_i = bf16(bf16(n_i cos_i) + bf16(rot(n)_i sin_i)).
@@ -260,6 +261,32 @@ __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
   }
 }
 
+// Device positions read by wave-uniform index with scalar loads. They
+// complete on the scalar counter, so waiting for them never waits for the
+// K/V loads issued before: vector loads complete in issue order, and a
+// position read as a plain load (the compiler cannot prove it unwritten by
+// the kernel's LDS-direct loads, so it becomes a vector load) makes the first
+// use wait for every load in flight. Positions are written by earlier
+// launches (or the host) and only read here.
+__device__ __forceinline__ int64_t load_pos(const int64_t* pos, int i) {
+  const int64_t* p = pos + i;
+  int64_t v;
+  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return v;
+}
+
+// pos[min(t, q - 1)] for t < kMaxQ: eight scalar loads in flight, one wait.
+__device__ __forceinline__ void load_pos8(const int64_t* pos, int q, int64_t (&v)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int64_t* p = pos + (t < q ? t : q - 1);
+    asm volatile("s_load_dwordx2 %0, %1, 0x0" : "=s"(v[t]) : "s"(p));
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+s"(v[0]), "+s"(v[1]), "+s"(v[2]), "+s"(v[3]), "+s"(v[4]), "+s"(v[5]),
+                 "+s"(v[6]), "+s"(v[7]));
+}
+
 struct AttnArgs {
   // queries [b, h, t, :] (unfused)
   const bf16_t* q; long q_sb, q_sh, q_st;
@@ -388,7 +415,12 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
         buffer_rsrc(a.part + orow * S * D, static_cast<uint32_t>(S) * D * 4);
     const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(a.ml + orow * S * 2, static_cast<uint32_t>(S) * 8);
     float nx, ny, den;
-    if (S <= 16) merge_row_short<16>(prs, mrs, S, lane, nx, ny, den);
+    // The fewest loads that cover the splits (each is a wave instruction
+    // even where the descriptor returns zeros).
+    if (S <= 8) merge_row_short<8>(prs, mrs, S, lane, nx, ny, den);
+    else if (S <= 16) merge_row_short<16>(prs, mrs, S, lane, nx, ny, den);
+    else if (S <= 24) merge_row_short<24>(prs, mrs, S, lane, nx, ny, den);
+    else if (S <= 32) merge_row_short<32>(prs, mrs, S, lane, nx, ny, den);
     else merge_row_short<48>(prs, mrs, S, lane, nx, ny, den);
     const int h = kvh * a.G + r / a.Q, t = r % a.Q;
     bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st;
@@ -496,9 +528,11 @@ __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   // Positions: scalar loads of pos[min(t, Q - 1)] (in bounds, branch-free).
   int qp[kMaxQ];
   int maxpos = -1;
+  int64_t pq[kMaxQ];
+  load_pos8(a.pos, a.Q, pq);
 #pragma unroll
   for (int t = 0; t < kMaxQ; ++t) {
-    const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+    const int64_t v = pq[t];
     // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
     const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
     qp[t] = t < a.Q ? vc : -1;
@@ -819,9 +853,11 @@ __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
 
   int qp[kMaxQ];
   int maxpos = -1;
+  int64_t pq[kMaxQ];
+  load_pos8(a.pos, a.Q, pq);
 #pragma unroll
   for (int t = 0; t < kMaxQ; ++t) {
-    const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+    const int64_t v = pq[t];
     // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
     const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
     qp[t] = t < a.Q ? vc : -1;
@@ -1067,7 +1103,7 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
     for (int t = 0; t < RING; ++t)
       stage_tile(krs0, vrs0, wave_ring + t * kLdsTile, lane, t * kSplit * D * 2 + wave_off);
   }
-  const int64_t pv = a.pos[0];
+  const int64_t pv = load_pos(a.pos, 0);
   const int pos = pv < 0 ? -1 : (pv >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(pv));
   const int last = pos < a.cap ? pos : static_cast<int>(a.cap) - 1;
   const int end = stop < last + 1 ? stop : last + 1;  // slots [start, end) are visible
@@ -1442,6 +1478,9 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
     }
     const int64_t v = a.pos[(tid < rows ? tid : 0) % a.Q];
     rpv = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
+    // Keep these loads ahead of the K/V staging: loads complete in issue
+    // order, so q issued behind the tiles would wait for all of them.
+    __builtin_amdgcn_sched_barrier(0);
   }
   // ---- 2. stage the first RING tiles at once, through descriptors over the
   // block's slots up to the capacity (slots past the newest position are
@@ -1473,15 +1512,17 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   int maxpos = -1, minpos = 1 << 30;
   if (MQ) {
     // Scalar loads of pos[min(t, Q - 1)] (in bounds, branch-free).
+    int64_t pq[kMaxQ];
+    load_pos8(a.pos, a.Q, pq);
 #pragma unroll
     for (int t = 0; t < kMaxQ; ++t) {
-      const int64_t v = a.pos[t < a.Q ? t : a.Q - 1];
+      const int64_t v = pq[t];
       const int vc = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
       maxpos = vc > maxpos ? vc : maxpos;
       minpos = vc < minpos ? vc : minpos;
     }
   } else {
-    const int64_t v = a.pos[0];
+    const int64_t v = load_pos(a.pos, 0);
     minpos = maxpos = v < 0 ? -1 : (v >= a.cap ? static_cast<int>(a.cap) : static_cast<int>(v));
   }
   const int pos = minpos;  // one query: its position
