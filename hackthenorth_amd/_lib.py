@@ -43,6 +43,8 @@ SIGNATURES = {
     "htn_gemv_norm": [_P, _P, _F, _P, _P, _I64, _I64, _I, _P],
     "htn_gemv_residual": [_P, _P, _P, _P, _I64, _I64, _P],
     "htn_lm_head_argmax": [_P, _P, _F, _P, _I64, _I64, _P, _P, _P, _P],
+    "htn_lm_head_argmax_noalloc": [_P, _P, _F, _P, _I64, _I64, _P, _P, _P],
+    "htn_head_scratch_capacity": [],
     "htn_gemv_w8": [_P, _P, _P, _I, _P, _I64, _I64, _P],
     "htn_gemv_norm_w8": [_P, _P, _F, _P, _P, _I, _P, _I64, _I64, _I, _P],
     "htn_gemv_residual_w8": [_P, _P, _P, _I, _P, _P, _I64, _I64, _P],
@@ -67,7 +69,8 @@ SIGNATURES = {
     "htn_xcc_ids": [_P, _I64, _P],
     "htn_attention_merge_in_kernel": [],
 }
-RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64}
+RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
+            "htn_head_scratch_capacity": _I64}
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX, EPI_RESIDUAL_NORM = 0, 1, 2, 3, 4
 
 _lib = None

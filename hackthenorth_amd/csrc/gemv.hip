@@ -701,3 +701,79 @@ extern "C" int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int6
                      static_cast<const bf16_t*>(logits), static_cast<long>(n), out);
   return launch_status();
 }
+
+// ------------------------------------------------------------------ allocation-free greedy head
+//
+// htn_lm_head_argmax_noalloc: htn_lm_head_argmax with its per-block keys in a
+// fixed device array instead of a caller buffer, for callers that cannot
+// allocate device memory. Every GPU the library runs on holds its own copy of
+// the array (HTN_HEAD_SCRATCH_BYTES, the most keys the head's grid writes)
+// until the process ends. Host code never passes the array's name to a
+// kernel: on the host it is only a stand-in for the symbol, so the device
+// address is looked up once per device with hipGetSymbolAddress and kept.
+
+static __device__ __align__(256) uint64_t htn_head_scratch[HTN_HEAD_SCRATCH_BYTES / 8];
+
+#include <mutex>
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_head_scratch_mu;
+void* g_head_scratch_ptr[kMaxDevices] = {};
+
+// Device address of htn_head_scratch on `device`, resolved on the first call
+// for that device with the device current; nullptr on failure.
+void* head_scratch_on(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_head_scratch_mu);
+  if (!g_head_scratch_ptr[device]) {
+    int current = -1;
+    if (hipGetDevice(&current) != hipSuccess) return nullptr;
+    if (current != device && hipSetDevice(device) != hipSuccess) return nullptr;
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(htn_head_scratch));
+    if (current != device) hipSetDevice(current);
+    if (rc != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_head_scratch_ptr[device] = p;
+  }
+  return g_head_scratch_ptr[device];
+}
+
+}  // namespace
+
+extern "C" int64_t htn_head_scratch_capacity(void) { return HTN_HEAD_SCRATCH_BYTES; }
+
+extern "C" int htn_lm_head_argmax_noalloc(const void* x, const void* gain, float eps,
+                                          const void* w, int64_t vocab, int64_t k,
+                                          int64_t* token_out, int64_t* position_inc,
+                                          htn_stream_t stream) {
+  if (!x || !w || !token_out || bad_sizes(vocab, k)) return HTN_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int device = -1;
+  if (st) {
+    if (hipStreamGetDevice(st, &device) != hipSuccess) return HTN_EINVAL;
+  } else if (hipGetDevice(&device) != hipSuccess) {
+    return HTN_ELAUNCH;
+  }
+  void* scratch = head_scratch_on(device);
+  if (!scratch) return HTN_ELAUNCH;
+  // The head's grid never exceeds kMaxBlocks keys (grid_for caps it), which
+  // is exactly the array's size; the check keeps that bound explicit.
+  static_assert(kMaxBlocks * 8 <= static_cast<long>(sizeof(htn_head_scratch)),
+                "greedy-head grid exceeds the fixed key array");
+  GemvArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.gain = static_cast<const bf16_t*>(gain);
+  a.w = static_cast<const bf16_t*>(w);
+  a.n = vocab;
+  a.k = static_cast<int>(k);
+  a.eps = eps;
+  a.token_out = token_out;
+  a.position_inc = position_inc;
+  a.partial = static_cast<uint64_t*>(scratch);
+  return gain ? dispatch<true, EPI_ARGMAX, WF_BF16>(a, st) : dispatch<false, EPI_ARGMAX, WF_BF16>(a, st);
+}

@@ -152,6 +152,25 @@ int htn_lm_head_argmax(const void* x, const void* gain, float eps, const void* w
                        int64_t vocab, int64_t k, int64_t* token_out,
                        int64_t* position_inc, void* scratch, htn_stream_t stream);
 
+/* htn_lm_head_argmax without the scratch argument: the per-block keys go to
+ * a fixed device array of HTN_HEAD_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends (its address is looked up once
+ * per device, on the first call there). Allocates nothing, so it can be
+ * called where hipMalloc cannot (under HIP graph capture, in serving loops
+ * that forbid allocation). Same results and limits as htn_lm_head_argmax
+ * (k <= 16384 and vocab <= 2^31, else HTN_EINVAL); the grid never writes
+ * more keys than the array holds. All calls on one GPU share the array, so
+ * calls that overlap on one GPU (concurrent streams) race; calls ordered on
+ * one stream do not. No initial contents are needed: every call writes each
+ * key it reads.
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate device memory. */
+int htn_lm_head_argmax_noalloc(const void* x, const void* gain, float eps, const void* w,
+                               int64_t vocab, int64_t k, int64_t* token_out,
+                               int64_t* position_inc, htn_stream_t stream);
+/* Bytes of the fixed key array above (HTN_HEAD_SCRATCH_BYTES). */
+int64_t htn_head_scratch_capacity(void);
+
 /* ---------------------------------------------------------------- 8-bit weights
  * Weight-only 8-bit twins of the four GEMVs above: w holds rows*k bytes in
  * `format` (HTN_WEIGHT_*), scales[n] is the fp32 scale of weight row n
