@@ -301,29 +301,39 @@ class DecodeState:
             self.step(model)
 
     def prefill(self, model, input_ids):
-        """Run the prompt through the decode step one token at a time.
+        """The whole prompt in one causal multi-row pass (decode.py:157-166).
 
-        Each replay attends over the slots written so far, which is the causal
-        prefill computed token by token; afterwards `token` holds the greedy
-        continuation and `position` equals the prompt length.
+        Every prompt token's K/V goes to its cache slot, the projections read
+        each weight once per 32 rows, attention is causal by absolute position,
+        and only the last row of each sequence reaches the LM head. Afterwards
+        `token` holds the greedy continuation and `position` equals the prompt
+        length. Launches only: it can be captured (prefill.prefill does).
         """
         batch, length = input_ids.shape
         if (batch, length) != self.shape[:2]:
             raise ValueError("prompt shape differs from the state's shape")
+        self.cache.prefill = True
+        token = forward(model, input_ids, self.cache, self.prompt_positions, rotary=self.rotary)
+        self.cache.prefill = False
+        self.token.copy_(token)
+        self.position.fill_(length)
+        return self.token
+
+    def prefill_stepwise(self, model, input_ids):
+        """The prompt through the captured decode step one token at a time (each
+        replay attends over the slots written so far): the same causal prefill
+        computed token by token, kept as a cross-check of the batched pass."""
+        batch, length = input_ids.shape
+        if (batch, length) != self.shape[:2] or batch != 1:
+            raise ValueError("stepwise prefill takes one prompt of the state's length")
         self.cache.prefill = False
         self.position.fill_(0)
-        if batch == 1:
-            for i in range(length):
-                self.token.copy_(input_ids[:, i:i + 1])
-                if self.graph is not None:
-                    self.graph.replay()
-                else:
-                    self.step(model)
-        else:
-            token = forward(model, input_ids, self.cache, self.prompt_positions,
-                            rotary=self.rotary)
-            self.token.copy_(token)
-            self.position.fill_(length)
+        for i in range(length):
+            self.token.copy_(input_ids[:, i:i + 1])
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self.step(model)
         return self.token
 
     def verify_step(self, model):

@@ -19,6 +19,7 @@ consumed dk, so the next cycle first steps it on dk.
 import torch
 
 from .decode import DecodeState
+from .prefill import prefill
 from .speculate import verified_tokens
 
 
@@ -69,8 +70,8 @@ class DraftSpeculator:
     def prefill(self, prompt):
         """Both models consume the prompt; returns the target's first token."""
         ids = torch.as_tensor(prompt, dtype=torch.int64, device=self.target.device).view(1, -1)
-        first = int(self.target_state.prefill(self.target, ids)[0, 0])
-        self.draft_state.prefill(self.draft, ids.to(self.draft.device))
+        first = int(prefill(self.target, self.target_state, ids)[0, 0])
+        prefill(self.draft, self.draft_state, ids.to(self.draft.device))
         return first
 
     def cycle(self, current, position, catch_up=None):

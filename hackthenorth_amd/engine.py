@@ -9,6 +9,7 @@ import torch
 from .decode import DecodeState, stream_decode
 from .draft import DraftSpeculator
 from .model import Qwen3Model
+from .prefill import prefill
 from .speculate import BackoffPromptLookup
 
 
@@ -50,7 +51,7 @@ class Engine:
                 self.state = DecodeState(self.model, *shape, speculative=self.speculative)
             state = self.state
             prompt = torch.tensor(input_ids, dtype=torch.int64, device=self.model.device)
-            current = state.prefill(self.model, prompt)
+            current = prefill(self.model, state, prompt)
             tokens = current[:, 0].tolist()
             if state.draft_tokens == 0:
                 yield from stream_decode(state, tokens, max_new_tokens)

@@ -43,6 +43,7 @@ from hackthenorth_amd.draft import DraftSpeculator
 from hackthenorth_amd.engine import Engine
 from hackthenorth_amd.kernels import rng as DR
 from hackthenorth_amd.kernels.greedy import greedy_head
+from hackthenorth_amd.prefill import prefill
 from hackthenorth_amd.model import (STREAM_LM_HEAD, STREAM_LM_HEAD_SCALE, Qwen3Model,
                                     shape_config, write_random_model_dir)
 from hackthenorth_amd.quant import QuantizedWeight
@@ -63,7 +64,7 @@ def check_hidden(label, actual, expected):
     exp = expected.detach().cpu().float().reshape(-1)
     err = float((act - exp).abs().max())
     scale = max(1.0, float(exp.abs().max()))
-    cos = float(torch.nn.functional.cosine_similarity(act, exp, dim=0))
+    cos = float(torch.nn.functional.cosine_similarity(act.double(), exp.double(), dim=0))
     print(f"{label}: max_abs_err={err:.4g} full_scale={scale:.4g} "
           f"normalised_err={err / scale:.3g} cos={cos:.7f}", flush=True)
     assert err <= 2e-2 * scale
@@ -204,6 +205,38 @@ def test_0p6b_decode_at_context_512_teacher_forced():
     for i, t in enumerate(emitted):
         record.add(i, logits[i], t)
     check_record(record, "0.6b ctx 512, 64 steps")
+
+
+def test_8b_prefill_2048_matches_oracle_batched_forward():
+    """The captured batched prefill of a 2048-token prompt (two 8B layers):
+    every prompt slot's K/V against the oracle's batched forward, the first
+    token against its logits, and a replay on a second prompt equal to the
+    eager pass on that prompt."""
+    layers, length = 2, 2048
+    oshape = dataclasses.replace(Q.SHAPES["8b"], layers=layers, vocab=64)
+    cfg = shape_config("qwen3-8b", num_hidden_layers=layers, vocab_size=64)
+    model = Qwen3Model.random(cfg)
+    oracle = Q.Oracle(oshape, Q.generate_weights(oshape, seed=0), length + 1)
+    prompts = [Q.prompt_ids(length, oshape.vocab, seed=s) for s in (1, 2)]
+    with torch.inference_mode():
+        state = D.DecodeState(model, 1, length, 2)
+        first = prefill(model, state, torch.tensor([prompts[0]], device="cuda"))
+        assert int(state.position) == length
+        ocache = Q.new_cache(oshape, length + 1)
+        _, logits, _ = oracle.forward(torch.tensor([prompts[0]]), ocache, torch.arange(length))
+        for layer in range(layers):
+            for kv, name in ((0, "k"), (1, "v")):
+                mine = state.cache.storage[layer, kv, 0, :, :length]
+                ref = (ocache.keys if kv == 0 else ocache.values)[layer][0, :, :length]
+                check_hidden(f"prefill 2048 layer {layer} {name} cache", mine, ref)
+        record = OP.TokenRecord(TOKEN_BAR)
+        record.add(0, logits[0, 0], int(first[0, 0]))
+        check_record(record, "8b prefill 2048 first token")
+        replayed = int(prefill(model, state, torch.tensor([prompts[1]], device="cuda"))[0, 0])
+        kv_replay = state.cache.storage[..., :length, :].clone()
+        eager = int(state.prefill(model, torch.tensor([prompts[1]], device="cuda"))[0, 0])
+        assert replayed == eager
+        assert torch.equal(kv_replay, state.cache.storage[..., :length, :])
 
 
 def golden(name):

@@ -63,7 +63,7 @@ def hidden_stats(actual, expected):
     act = actual.detach().cpu().float().reshape(-1)
     exp = expected.detach().cpu().float().reshape(-1)
     err = (act - exp).abs()
-    cos = float(torch.nn.functional.cosine_similarity(act, exp, dim=0))
+    cos = float(torch.nn.functional.cosine_similarity(act.double(), exp.double(), dim=0))
     return act, exp, err, cos
 
 

@@ -165,7 +165,7 @@ def test_w8_layers_and_teacher_forced_ids_match_oracle(fmt):
             mine = D.decode_layer(model, layer, h, cache, pos, rotary)
             exp = oracle.layer(layer, h.cpu().view(1, 1, -1), ocache, torch.tensor([last]))
             a, e = mine.cpu().float().reshape(-1), exp.float().reshape(-1)
-            cos = float(torch.nn.functional.cosine_similarity(a, e, dim=0))
+            cos = float(torch.nn.functional.cosine_similarity(a.double(), e.double(), dim=0))
             print(f"{fmt} layer {layer}: max|err|={float((a - e).abs().max()):.4g} "
                   f"max|h|={float(e.abs().max()):.4g} cos={cos:.7f}", flush=True)
             torch.testing.assert_close(a, e, atol=2e-2, rtol=2e-2)
