@@ -389,6 +389,8 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   if (epilogue < HTN_EPI_STORE || epilogue > HTN_EPI_ARGMAX) return HTN_EINVAL;
   if (epilogue == HTN_EPI_ARGMAX ? !tokens : !y) return HTN_EINVAL;
   if (epilogue == HTN_EPI_RESIDUAL && !residual) return HTN_EINVAL;
+  // Output and residual rows must not overlap.
+  if (y && (y_stride < n || (epilogue == HTN_EPI_RESIDUAL && res_stride < n))) return HTN_EINVAL;
   // 16-byte fragments of x, gain and W rows.
   if (k % kStep || k > kMaxK || x_stride % 8 || !aligned16(x) || !aligned16(w) ||
       (gain && !aligned16(gain)))
@@ -429,6 +431,7 @@ extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, cons
   if (!x || !w || !residual || !y || !gain || !normed || rows <= 0 || rows > kMaxRowsMT ||
       n <= 0 || k <= 0 || n > (1L << 31))
     return HTN_EINVAL;
+  if (y_stride < n || res_stride < n) return HTN_EINVAL;  // rows must not overlap
   if (k % kStep || k > kMaxK) return HTN_EUNSUPPORTED;
   const Plan p = plan_residual_norm(rows, n, k);
   // The finish holds a row of y in LDS: 8-element vectors, at most 8192 columns.

@@ -37,15 +37,23 @@ def greedy_head(x, gain, eps, w, out, advance=None):
 
 
 def greedy_token(x, w):
-    """argmax over bf16(x @ w.T) per row, lowest id on ties; returns x.shape[:-1] int64."""
+    """argmax over bf16(x @ w.T) per row, lowest id on ties; returns x.shape[:-1] int64.
+
+    One row takes the batch-one head; several rows read the vocabulary
+    weight once per 32 rows (greedy.py:45-60 reads it once for up to 32).
+    """
     k = x.shape[-1]
-    if w.shape[1] != k or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+    if w.dim() != 2 or w.shape[1] != k or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise ValueError("greedy_token expects bfloat16 rows and a [V, K] weight")
+    _lib.require_gpu(x, w)
     rows = x.reshape(-1, k).contiguous()
-    out = torch.empty((rows.shape[0],), dtype=torch.int64, device=x.device)
-    for r in range(rows.shape[0]):
-        greedy_head(rows[r], None, 0.0, w.contiguous(), out[r:r + 1])
-    return out.reshape(x.shape[:-1])
+    weight = w.contiguous()
+    if rows.shape[0] == 1:
+        out = torch.empty((1,), dtype=torch.int64, device=x.device)
+        greedy_head(rows[0], None, 0.0, weight, out)
+        return out.reshape(x.shape[:-1])
+    from .rows import greedy_rows
+    return greedy_rows(rows, weight).reshape(x.shape[:-1])
 
 
 def argmax(logits):

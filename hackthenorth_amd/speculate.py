@@ -1,9 +1,17 @@
 """Prompt-lookup drafts and exact greedy verification (dryft/engine/speculate.py).
 
-The acceptance rule is part of the output contract: a draft token is kept
-only while it equals the target's greedy prediction, and exactly one target
-token (the correction, or the bonus after a full match) follows the accepted
-prefix (speculate.py:55-69).
+The behaviour is the reference's contract, the one its tests pin
+(dryft/tests/test_speculate.py:10-63): a lookup proposes the continuation
+that followed the latest earlier occurrence of the current n-gram, counting
+only occurrences whose whole continuation is already known, and a draft token
+is kept only while it equals the target's greedy prediction, with exactly one
+target token (correction or bonus) after the accepted prefix
+(speculate.py:55-69).
+
+The index here is maintained as tokens arrive: appending a token makes one
+more occurrence old enough to have a full continuation, and that occurrence
+(the newest of its n-gram) overwrites the n-gram's entry, so a proposal is one
+dictionary lookup.
 """
 
 #: Draft width of the reference's verifier (speculate.py:3).
@@ -16,36 +24,40 @@ def draft_width(output_length):
 
 
 class PromptLookup:
-    """Propose the continuation of the most recent earlier occurrence of the
-    last `ngram` tokens (speculate.py:11-33).
+    """n-gram prompt lookup over a growing token history (speculate.py:11-33).
 
-    The index maps each n-gram to the position right after its latest
-    occurrence whose continuation of `draft_length` tokens is fully known;
-    it is extended incrementally as tokens are appended.
+    `_next[gram]` is the index right after the newest occurrence of `gram`
+    that starts at least `ngram + draft_length` tokens before the end of the
+    history, so its `draft_length` continuation tokens all exist.
     """
 
     def __init__(self, prompt, draft_length=DRAFT_TOKENS, ngram=4):
-        self.tokens = list(prompt)
-        self.draft_length = draft_length
         self.ngram = ngram
-        self._indexed = 0          # occurrences starting before this are indexed
-        self._after = {}
+        self.draft_length = draft_length
+        self.tokens = []
+        self._next = {}
+        for token in prompt:
+            self.append(token)
 
     def append(self, token):
         self.tokens.append(token)
+        # The occurrence starting here has just become complete (n-gram plus
+        # draft_length continuation tokens); a later one of the same n-gram
+        # replaces it when it completes.
+        start = len(self.tokens) - self.ngram - self.draft_length
+        if start >= 0:
+            gram = tuple(self.tokens[start:start + self.ngram])
+            self._next[gram] = start + self.ngram
 
     def propose(self):
-        n, width = self.ngram, self.draft_length
-        limit = len(self.tokens) - n - width + 1
-        for start in range(self._indexed, limit):
-            self._after[tuple(self.tokens[start:start + n])] = start + n
-        self._indexed = max(self._indexed, limit)
-        if len(self.tokens) < n:
+        """The draft (draft_length tokens) or None when the current n-gram has
+        no complete earlier occurrence."""
+        if len(self.tokens) < self.ngram:
             return None
-        follow = self._after.get(tuple(self.tokens[-n:]))
+        follow = self._next.get(tuple(self.tokens[-self.ngram:]))
         if follow is None:
             return None
-        return self.tokens[follow:follow + width]
+        return self.tokens[follow:follow + self.draft_length]
 
 
 class BackoffPromptLookup:
@@ -69,11 +81,16 @@ class BackoffPromptLookup:
 def verified_tokens(proposal, predictions):
     """Accepted draft prefix plus one target token (speculate.py:55-69).
 
-    predictions[i] is the target's greedy token after current + proposal[:i].
+    predictions[i] is the target's greedy token after current + proposal[:i];
+    the first draft that differs from its prediction ends the accepted prefix,
+    and that prediction is the correction (after a full match, the last
+    prediction is the bonus). Predictions past a rejected draft were computed
+    on tokens that will not be emitted and are dropped.
     """
     if len(predictions) != len(proposal) + 1:
-        raise ValueError("verification needs one prediction per draft token plus a bonus")
-    accepted = 0
-    while accepted < len(proposal) and proposal[accepted] == predictions[accepted]:
-        accepted += 1
-    return list(predictions[:accepted + 1])
+        raise ValueError(f"{len(proposal)} draft tokens need {len(proposal) + 1} target "
+                         f"predictions, got {len(predictions)}")
+    for i, draft in enumerate(proposal):
+        if predictions[i] != draft:
+            return list(predictions[:i + 1])
+    return list(predictions)

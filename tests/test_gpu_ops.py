@@ -150,6 +150,19 @@ def test_greedy_head_ties_choose_lowest_id():
     assert G.greedy_token(x, w).tolist() == [[3], [3], [3]]
 
 
+@pytest.mark.parametrize("rows", [2, 5, 8, 20])
+def test_greedy_token_rows_read_the_head_once_and_match_oracle(rows):
+    """The reference signature at verify shapes (8 rows is dryft's verifier):
+    several rows go through one multi-row launch per 32 rows."""
+    v, k = 151936, 2560
+    w = nrm(21, (v, k), std=0.02)
+    x = nrm(22, (rows, k))
+    got = G.greedy_token(cuda(x), cuda(w)).tolist()
+    logits = x.float() @ w.float().T
+    for r in range(rows):
+        _assert_argmax(got[r], logits[r])
+
+
 def test_greedy_head_matches_oracle_argmax():
     v, k = 151936, 1024
     w = nrm(14, (v, k), std=0.02)
