@@ -19,6 +19,7 @@ HTN_EINVAL = -1
 HTN_EUNSUPPORTED = -2
 HTN_ELAUNCH = -3
 HEAD_SCRATCH_BYTES = 65536
+ATTENTION_XCD_MISMATCH_BYTE = 8  # HTN_ATTENTION_XCD_MISMATCH_BYTE
 HEAD_DIM = 128
 
 _P = ctypes.c_void_p

@@ -33,11 +33,17 @@ constexpr int kMinSplit = 16;       // fewest slots a block is given
 constexpr int kMaxQ = 8;            // queries per launch (verify rows)
 constexpr int kMergeUnroll = 16;    // partials loaded back to back in the merge
 // Arrival counters of the in-kernel merge, at the head of the scratch buffer:
-// one 128-byte line per (batch, kv head) pair.
+// one 128-byte line per (batch, kv head) pair, a 64-bit counter at its start.
 constexpr int kCounterStride = 32;  // uint32 words
 constexpr int kMaxCounterPairs = 256;
 constexpr long kCounterBytes = static_cast<long>(kMaxCounterPairs) * kCounterStride * 4;
 static_assert(kCounterBytes == HTN_ATTENTION_COUNTER_BYTES, "counter region size");
+// Pair p's 64-bit counter sits at the start of its 128-byte line; the XCD
+// mismatch count is the 32-bit word right after pair 0's counter.
+constexpr long kXcdMismatchByte = HTN_ATTENTION_XCD_MISMATCH_BYTE;
+static_assert(kXcdMismatchByte >= 8 && kXcdMismatchByte + 4 <= kCounterStride * 4,
+              "mismatch word inside pair 0's line, past its counter");
+static_assert(48 < 64, "six bits per XCD hold up to 48 splits");
 static_assert(kMaxQ == 8, "load_pos8 reads eight positions");
 
 // Per-head RMSNorm then RoPE (rotate_half), reference rounding:
@@ -396,14 +402,35 @@ __device__ __forceinline__ void merge_row_short(__amdgpu_buffer_rsrc_t prs, __am
 //   out = sum_s w_s acc_s / sum_s w_s l_s,  w_s = exp(m_s - M),  M = max_s m_s.
 // Every load of a row is in flight at once (the host takes this path for at
 // most four rows of at most 48 splits).
+//
+// The pair's 64-bit counter holds one 6-bit arrival count per XCD: a split
+// adds 1 << (6 * its XCC_ID), so the block that completes the count also
+// sees where every split ran. Were any split of the pair on another XCD
+// than the merging block (dispatch not round-robin), its partial might not be
+// visible in this L2: the merge still runs, and the mismatch count at byte
+// kXcdMismatchByte of the counters is incremented for the host to read.
 __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, int* last) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   const int p = b * a.Hkv + kvh;
-  unsigned* cnt = a.done + static_cast<long>(p) * kCounterStride;
-  if (threadIdx.x == 0)
-    *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            static_cast<unsigned>(a.splits - 1);
+  unsigned long long* cnt =
+      reinterpret_cast<unsigned long long*>(a.done + static_cast<long>(p) * kCounterStride);
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7u;
+    const unsigned long long mine = 1ull << (6 * xcc);
+    const unsigned long long total =
+        __hip_atomic_fetch_add(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    unsigned arrived = 0;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) arrived += static_cast<unsigned>(total >> (6 * x)) & 63u;
+    const bool done = arrived == static_cast<unsigned>(a.splits);
+    *last = done;
+    if (done && total != static_cast<unsigned long long>(a.splits) << (6 * xcc))
+      __hip_atomic_fetch_add(a.done + kXcdMismatchByte / 4, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
   if (!*last) return;
   // A wave-uniform row index keeps the row's descriptors in scalar registers.
@@ -426,7 +453,7 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
     bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st;
     *reinterpret_cast<uint32_t*>(dst + 2 * lane) = pack_bf2(nx / den, ny / den);
   }
-  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Query source of the partial kernel: q rows from memory, or the fused

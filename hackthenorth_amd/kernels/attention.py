@@ -35,6 +35,28 @@ def _scratch(device, batch, heads, queries, capacity):
     return buffer
 
 
+def xcd_merge_mismatches(device=None, reset=False):
+    """How many in-kernel split merges found a split of their (batch, kv head)
+    pair on another XCD than their own, summed over the attention scratch
+    buffers kept for `device` (0 on a correct run: the merge relies on
+    round-robin workgroup dispatch to keep a pair's partials in one L2).
+    Reads device memory, so it synchronises; reset=True clears the counts."""
+    index = torch.device(device).index if device is not None else torch.cuda.current_device()
+    if index is None:
+        index = torch.cuda.current_device()
+    word = _lib.ATTENTION_XCD_MISMATCH_BYTE // 4
+    total = 0
+    for (dev, _stream), buffers in _SCRATCH.items():
+        if dev != index:
+            continue
+        for buffer in buffers:
+            count = buffer.view(torch.int32)[word]
+            total += int(count)
+            if reset:
+                count.zero_()
+    return total
+
+
 def _check_cache(keys, values, batch, kv_heads):
     if keys.shape != values.shape or keys.dim() != 4 or keys.shape[0] != batch \
             or keys.shape[1] != kv_heads or keys.shape[3] != _lib.HEAD_DIM \

@@ -267,6 +267,13 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
  * buffer is allocated; every call leaves them zero. Calls sharing a scratch
  * buffer must be ordered (one stream). */
 #define HTN_ATTENTION_COUNTER_BYTES 32768
+/* Byte offset, inside the counter region, of a 32-bit count of in-kernel
+ * merges that found a split of their (batch, kv head) pair on another XCD
+ * than their own (dispatch not round-robin, so that split's partial may not
+ * have been visible to the merge). It stays 0 on a correct run and, unlike the
+ * arrival counters, is never reset by the kernels: the caller reads it (any
+ * time after the calls it covers) and clears it. */
+#define HTN_ATTENTION_XCD_MISMATCH_BYTE 8
 int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap);
 
 /* Grouped-query attention over fixed-capacity caches with causality by

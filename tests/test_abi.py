@@ -54,3 +54,12 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.htn_gemv_w8(one, one, one, 3, one, 16, 16, null) == _lib.HTN_EINVAL
     assert lib.htn_gemv_w8(one, one, null, 1, one, 16, 16, null) == _lib.HTN_EINVAL
     assert lib.htn_fill_weights_w8(one, 16, 0, 0, 0, null) == _lib.HTN_EINVAL
+
+
+def test_header_constants_match_the_binding():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (HTN_\w+) \(?(-?\d+)\)?", text))
+    assert int(consts["HTN_HEAD_SCRATCH_BYTES"]) == _lib.HEAD_SCRATCH_BYTES
+    assert int(consts["HTN_ATTENTION_XCD_MISMATCH_BYTE"]) == _lib.ATTENTION_XCD_MISMATCH_BYTE
+    assert int(consts["HTN_EINVAL"]) == _lib.HTN_EINVAL
+    assert int(consts["HTN_HEAD_DIM"]) == _lib.HEAD_DIM

@@ -195,10 +195,15 @@ def test_0p6b_decode_at_context_512_teacher_forced():
     prompt_len, steps = 512, 64
     prompt = Q.prompt_ids(prompt_len, shape.vocab)
     model = Qwen3Model.random(shape_config("qwen3-0.6b"))
+    from hackthenorth_amd.kernels import attention as A
+    A.xcd_merge_mismatches(reset=True)
     with torch.inference_mode():
         state = D.DecodeState(model, 1, prompt_len, steps)
         first = state.prefill(model, torch.tensor([prompt], device="cuda"))[:, 0].tolist()
         emitted = [t[0] for t in D.stream_decode(state, first, steps)]
+    # Every in-kernel split merge of the 64 captured steps saw its pair's
+    # splits on its own XCD.
+    assert A.xcd_merge_mismatches() == 0
     oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), prompt_len + steps)
     logits = oracle.teacher_forced_logits(prompt, emitted)
     record = OP.TokenRecord(TOKEN_BAR)

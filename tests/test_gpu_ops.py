@@ -312,6 +312,23 @@ def test_xcd_dispatch_keeps_block_columns_on_one_xcd():
           lib.htn_attention_merge_in_kernel())
 
 
+def test_xcd_mismatch_count_reads_and_resets_from_the_host():
+    """The reader of the merge's XCD-mismatch word, with the word set from the
+    host (no kernel is made to mismatch): it sums the word over the scratch
+    buffers kept for the device and clears it on request."""
+    q = cuda(nrm(39, (1, 8, 1, 128)))
+    k, v = cuda(nrm(40, (1, 2, 600, 128))), cuda(nrm(41, (1, 2, 600, 128)))
+    A.grouped_attention(q, k, v, torch.tensor([500], device="cuda"))
+    torch.cuda.synchronize()
+    A.xcd_merge_mismatches(reset=True)
+    buffer = A._SCRATCH[(torch.cuda.current_device(),
+                         torch.cuda.current_stream().cuda_stream)][-1]
+    buffer.view(torch.int32)[_lib.ATTENTION_XCD_MISMATCH_BYTE // 4] = 3
+    assert A.xcd_merge_mismatches() == 3
+    assert A.xcd_merge_mismatches(reset=True) == 3
+    assert A.xcd_merge_mismatches() == 0
+
+
 @pytest.mark.parametrize("batch,heads,kv_heads,position,capacity",
                          [(1, 4, 1, 700, 1000), (3, 8, 2, 300, 600), (3, 16, 4, 1500, 2100),
                           (5, 8, 8, 90, 200), (2, 8, 8, 5000, 8200)])
