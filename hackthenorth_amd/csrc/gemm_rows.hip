@@ -286,6 +286,122 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_argmax(const uint64_t* __res
   }
 }
 
+// ------------------------------------------------------------------ interleaved gate/up
+// SwiGLU of x by a K-major weight w[K, 2I] whose row k holds (gate_i, up_i)
+// pairs: w[k, 2i] = gate_i[k], w[k, 2i + 1] = up_i[k] (the reference's
+// offline layout). A block owns a strip of 32 outputs, i.e. 128 contiguous
+// bytes of every weight row; lane (c, q) = (lane & 15, lane >> 4) loads
+// 8 bytes, (gate, up) of outputs 2c and 2c + 1, from each of the rows
+// q*8 .. q*8 + 7 of a 32-row step, so every load instruction reads four whole
+// 128-byte row segments. The eight words per lane regroup in registers into
+// the B fragments of four MFMAs (gate and up of the even outputs 2c, and of
+// the odd outputs 2c + 1: output tile t holds outputs 2c + t), with k
+// q*8 .. q*8 + 7 in lane quad q of both operands. Waves take interleaved
+// steps, reduce through LDS and finish as gemm_rows_kernel does (K-split
+// partials in its [KS][M][2I] gate-then-up layout).
+constexpr int kStepI = 32;     // k per step: one MFMA depth
+constexpr int kStripI = 32;    // outputs per block: two 16-output tiles
+constexpr int kUI = 2;         // steps in flight per wave
+
+template <int MT, int W>
+__global__ __launch_bounds__(W * 64) void gemm_rows_interleaved(RowsArgs a) {
+  __shared__ float red[W][MT][4][16 * 16];  // [wave][row tile][tile t, gate/up][row][col]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int strip = blockIdx.x, ks = blockIdx.y;
+  const int n0 = strip * kStripI;
+  const int col = lane & 15, quad = lane >> 4;
+  const int j0 = ks * a.steps_per_split;
+  const int total_steps = a.K / kStepI;
+  const int j1 = j0 + a.steps_per_split < total_steps ? j0 + a.steps_per_split : total_steps;
+
+  // The lane's output pair (2c, 2c + 1), clamped to the last pair (a.N is
+  // even; clamped lanes compute discarded outputs).
+  const int pair = n0 + 2 * col < a.N ? n0 + 2 * col : a.N - 2;
+  const long row_len = 2L * a.N;
+  const bf16_t* wlane = a.w + static_cast<long>(quad) * 8 * row_len + 2L * pair;
+
+  uint2 wv[kUI][8];
+  auto issue = [&](int jb) {
+#pragma unroll
+    for (int u = 0; u < kUI; ++u) {
+      int j = jb + u * W;
+      j = j < j1 ? j : j1 - 1;
+      const bf16_t* p = wlane + static_cast<long>(j) * kStepI * row_len;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) wv[u][r] = *reinterpret_cast<const uint2*>(p + r * row_len);
+    }
+  };
+  issue(j0 + wave);
+
+  f32x4_t acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[t][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int jb = j0 + wave; jb < j1; jb += W * kUI) {
+    if (jb != j0 + wave) issue(jb);
+#pragma unroll
+    for (int u = 0; u < kUI; ++u) {
+      const int j = jb + u * W;
+      const bool ok = j < j1;
+      const int k = (ok ? j : j1 - 1) * kStepI + quad * 8;
+      uint4 av[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) av[t] = a_fragment(a, t * 16 + col, k, ok);
+      // Fragments f = 2 * tile + (0 gate, 1 up): word x of row r holds
+      // (gate, up) of output 2c, word y of output 2c + 1.
+      uint4 b[4];
+      uint32_t* bw = reinterpret_cast<uint32_t*>(b);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint2 lo = wv[u][2 * d], hi = wv[u][2 * d + 1];
+        bw[0 * 4 + d] = (lo.x & 0xffffu) | (hi.x << 16);
+        bw[1 * 4 + d] = (lo.x >> 16) | (hi.x & 0xffff0000u);
+        bw[2 * 4 + d] = (lo.y & 0xffffu) | (hi.y << 16);
+        bw[3 * 4 + d] = (lo.y >> 16) | (hi.y & 0xffff0000u);
+      }
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+          acc[t][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, av[t]), __builtin_bit_cast(bf16x8_t, b[f]), acc[t][f],
+              0, 0, 0);
+    }
+  }
+
+  // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + i.
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][f][(quad * 4 + i) * 16 + col] = acc[t][f][i];
+  __syncthreads();
+
+  // tid -> (row m, strip output o); output o is column o >> 1 of tile o & 1.
+  const int Nw = 2 * a.N;
+  for (int idx = tid; idx < MT * 16 * kStripI; idx += W * 64) {
+    const int m = idx / kStripI, o = idx % kStripI;
+    const int t = m / 16, r = m % 16, tile = o & 1, c = o >> 1;
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < W; ++ww) {
+      g += red[ww][t][2 * tile][r * 16 + c];
+      u += red[ww][t][2 * tile + 1][r * 16 + c];
+    }
+    const int n = n0 + o;
+    if (m >= a.M || n >= a.N) continue;
+    if (a.KS > 1) {
+      a.part[(static_cast<long>(ks) * a.M + m) * Nw + n] = g;
+      a.part[(static_cast<long>(ks) * a.M + m) * Nw + a.N + n] = u;
+    } else {
+      store_out<HTN_EPI_SWIGLU>(a, m, n, g, u);
+    }
+  }
+}
+
 // Waves per strip: enough for about 16 waves per CU, 4 to 16 per block, and
 // at least two k steps per wave. K splits across blocks only when 16 waves
 // per strip still leave the GPU under-filled.
@@ -363,6 +479,48 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
 // rows 6-7% slower): the split projection loses more than the norm launch
 // costs, and a 4096-wide row is too long for one wave's finish.
 Plan plan_residual_norm(long M, long N, long K) { return plan(M, N, K, HTN_EPI_RESIDUAL, false); }
+
+// The interleaved gate/up kernel's plan, by the same rule over 32-row steps
+// and 32-output strips; two row tiles keep to 8 waves (64 KB of LDS).
+Plan plan_interleaved(long M, long N, long K) {
+  Plan p{};
+  const long strips = (N + kStripI - 1) / kStripI;
+  const long steps = K / kStepI;
+  const long target = 16L * device_cus();
+  const int max_w = M > 16 ? 8 : kMaxWaves;
+  int w = 4;
+  while (w < max_w && strips * w < target && steps >= 4L * w) w *= 2;
+  long ks = (target + strips * w - 1) / (strips * w);
+  const long max_ks = steps / (4L * w) > 0 ? steps / (4L * w) : 1;
+  if (ks > max_ks) ks = max_ks;
+  if (ks > 8) ks = 8;
+  p.waves = w;
+  p.ks = static_cast<int>(ks < 1 ? 1 : ks);
+  p.tail_bytes = p.ks > 1 ? static_cast<long>(p.ks) * M * N * 2 * 4 : 0;
+  return p;
+}
+
+template <int MT, int W>
+int launch_interleaved_w(RowsArgs& a, hipStream_t st) {
+  const int strips = (a.N + kStripI - 1) / kStripI;
+  hipLaunchKernelGGL((gemm_rows_interleaved<MT, W>), dim3(strips, a.KS), dim3(W * 64), 0, st, a);
+  if (launch_status() != HTN_OK) return HTN_ELAUNCH;
+  if (a.KS > 1) {
+    const long outs = static_cast<long>(a.M) * a.N;
+    hipLaunchKernelGGL((gemm_rows_finish<2, HTN_EPI_SWIGLU>),
+                       dim3((outs + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);
+  }
+  return launch_status();
+}
+
+template <int MT>
+int launch_interleaved(RowsArgs& a, int waves, hipStream_t st) {
+  if constexpr (MT == 1) {
+    if (waves >= 16) return launch_interleaved_w<MT, 16>(a, st);
+  }
+  if (waves >= 8) return launch_interleaved_w<MT, 8>(a, st);
+  return launch_interleaved_w<MT, 4>(a, st);
+}
 
 }  // namespace
 }  // namespace htn
@@ -464,4 +622,34 @@ extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, cons
   a.normed = static_cast<bf16_t*>(normed);
   if (rows <= 16) return launch<1, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
   return launch<2, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+}
+
+extern "C" int64_t htn_gate_up_swiglu_scratch_bytes(int64_t rows, int64_t width, int64_t k) {
+  if (rows <= 0 || rows > kMaxRowsMT || width <= 0 || width % 2 || k <= 0 || k % kStepI) return 0;
+  return plan_interleaved(rows, width, k).tail_bytes;
+}
+
+extern "C" int htn_gate_up_swiglu(const void* x, int64_t x_stride, const void* w, int64_t width,
+                                  int64_t k, int64_t rows, void* y, int64_t y_stride,
+                                  void* scratch, htn_stream_t stream) {
+  if (!x || !w || !y || rows <= 0 || rows > kMaxRowsMT || width <= 0 || k <= 0 ||
+      width > (1L << 30) || y_stride < width)
+    return HTN_EINVAL;
+  // 16-byte rows of x, 8-byte (gate, up) pairs of w; every step 32 rows of w.
+  if (width % 2 || k % kStepI || k > (1L << 24) || x_stride % 8 || x_stride < k ||
+      !aligned16(x) || !aligned8(w))
+    return HTN_EUNSUPPORTED;
+  const Plan p = plan_interleaved(rows, width, k);
+  if (p.tail_bytes > 0 && !scratch) return HTN_EINVAL;
+  RowsArgs a{};
+  a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
+  a.w = static_cast<const bf16_t*>(w);
+  a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
+  a.M = static_cast<int>(rows); a.N = static_cast<int>(width); a.K = static_cast<int>(k);
+  a.KS = p.ks;
+  a.steps_per_split = (a.K / kStepI + a.KS - 1) / a.KS;
+  a.part = static_cast<float*>(scratch);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows <= 16) return launch_interleaved<1>(a, p.waves, st);
+  return launch_interleaved<2>(a, p.waves, st);
 }

@@ -733,8 +733,8 @@ void* head_scratch_on(int device) {
     if (current != device && hipSetDevice(device) != hipSuccess) return nullptr;
     void* p = nullptr;
     const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(htn_head_scratch));
-    if (current != device) hipSetDevice(current);
-    if (rc != hipSuccess || !p) {
+    const bool restored = current == device || hipSetDevice(current) == hipSuccess;
+    if (rc != hipSuccess || !p || !restored) {
       (void)hipGetLastError();
       return nullptr;
     }

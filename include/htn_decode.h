@@ -235,6 +235,22 @@ int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w, 
                                 int64_t res_stride, void* y, int64_t y_stride, const void* gain,
                                 float eps, void* normed, void* scratch, htn_stream_t stream);
 
+/* SwiGLU of `rows` (1..32) activation rows x[m, :k] (row stride x_stride)
+ * by the interleaved K-major weight w[k, 2 * width] (row-major, w[k, 2i] the
+ * gate and w[k, 2i + 1] the up weight of output i):
+ *   y[m, i] = bf16(bf16(silu(bf16(gate))) * bf16(up))   (row stride y_stride)
+ * read in place, the weight once for all rows (MFMA tiles). k must be a
+ * multiple of 32, width even, x (with its stride) 16-byte and w 8-byte
+ * aligned.
+ * scratch: htn_gate_up_swiglu_scratch_bytes(rows, width, k) bytes (K-split
+ * partials; 0 means none is needed).
+ * Replaces the reference's gate_up_swiglu (dryft/engine/kernels/gateup.py:40-58)
+ * on its own weight layout. */
+int64_t htn_gate_up_swiglu_scratch_bytes(int64_t rows, int64_t width, int64_t k);
+int htn_gate_up_swiglu(const void* x, int64_t x_stride, const void* w, int64_t width, int64_t k,
+                       int64_t rows, void* y, int64_t y_stride, void* scratch,
+                       htn_stream_t stream);
+
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
                     htn_stream_t stream);
