@@ -7,12 +7,18 @@
 //
 //  * block = W waves (4 to 16, more when strips are few) on one 16-column
 //    strip (plus the matching up strip for SwiGLU); the waves take
-//    interleaved 64-wide k steps, each lane loading 32 contiguous bytes of one
-//    weight row per step (a 16-row x 128-byte tile per step, whole cache
-//    lines per wave), U steps in flight, and reduce through LDS, so every
-//    output is finished by the block that computed it. Within a step the two
-//    MFMAs see k permuted identically in A and B (lane quad q holds k offsets
-//    16q .. 16q+15), which leaves each dot product unchanged;
+//    interleaved 64-wide k steps and reduce through LDS, so every output is
+//    finished by the block that computed it. A step's 16-row x 128-byte
+//    weight tile is loaded as two instructions of 8 whole rows x 128 bytes
+//    (lane l: row l / 8, bytes 16 * (l % 8)), then regrouped through the
+//    wave's own LDS tile into the MFMA layout (lane (c, q): row c, bytes
+//    32q .. 32q + 31). Loading the MFMA layout directly spreads each
+//    instruction's 64 lanes over 16 rows, twice the cache lines per byte of
+//    whole-line loads, and the vector memory path, not HBM, then limits the
+//    stream; the LDS round trip costs far less. Within a step the two MFMAs
+//    see k permuted identically
+//    in A and B (lane quad q holds k offsets 16q .. 16q+15), which leaves
+//    each dot product unchanged;
 //  * only when even 16 waves per strip cannot fill the GPU is K split over
 //    KS blocks, whose fp32 partials a second, stream-ordered launch sums in a
 //    fixed order (deterministic) before the epilogue;
@@ -32,7 +38,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kStrip = 16;     // output columns per block (MFMA N)
 constexpr int kStep = 64;      // k per step: two MFMAs of 32
 constexpr int kMaxRowsMT = 32; // two 16-row tiles
-constexpr int kU = 2;          // k steps (32 bytes per lane per weight row) in flight per wave
+constexpr int kU = 1;          // k steps per wave per batch (1 measured fastest of 1, 2, 4)
 constexpr int kMaxWaves = 16;
 constexpr int kMaxK = 16384;
 
@@ -75,10 +81,13 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, int m, int n, float
   a.y[m * a.y_rs + n] = static_cast<bf16_t>(f2bf(out));
 }
 
+constexpr int kPitch = 144;  // bytes per staged 64-element weight row (+16: conflict-free reads)
+
 template <int MT, int S, int EPI, int W>
 __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   __shared__ float red[W][MT][S][kStrip * 16];
   __shared__ uint64_t best[kMaxRowsMT][kStrip];
+  __shared__ __align__(16) unsigned char tile[W][16 * kPitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int strip = blockIdx.x, ks = blockIdx.y;
   const int n0 = strip * kStrip;
@@ -88,28 +97,36 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   const int total_steps = a.K / kStep;
   const int j1 = j0 + a.steps_per_split < total_steps ? j0 + a.steps_per_split : total_steps;
 
-  // Weight rows of this lane (clamped to the last row; extra columns are discarded).
-  const bf16_t* wrow[S];
+  // Load mapping: lane l reads 16 bytes (chunk l & 7) of strip rows l >> 3
+  // and (l >> 3) + 8, clamped to the last row (extra columns are discarded).
+  const int lr = lane >> 3, lc = lane & 7;
+  const bf16_t* wrow[S][2];
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const int n = n0 + col < a.N ? n0 + col : a.N - 1;
-    wrow[s] = a.w + static_cast<long>(n + s * a.N) * a.K + quad * 16;
-  }
-
-  uint4 wv[kU][S][2];
-  auto issue = [&](int jb) {
+  for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      int j = jb + u * W;
-      j = j < j1 ? j : j1 - 1;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        wv[u][s][0] = *reinterpret_cast<const uint4*>(wrow[s] + j * kStep);
-        wv[u][s][1] = *reinterpret_cast<const uint4*>(wrow[s] + j * kStep + 8);
-      }
+    for (int h = 0; h < 2; ++h) {
+      const int n = n0 + lr + 8 * h < a.N ? n0 + lr + 8 * h : a.N - 1;
+      wrow[s][h] = a.w + static_cast<long>(n + s * a.N) * a.K + lc * 8;
     }
-  };
-  issue(j0 + wave);
+  unsigned char* wt = tile[wave];
+  u32x4* wr0 = reinterpret_cast<u32x4*>(wt + lr * kPitch + lc * 16);
+  u32x4* wr1 = reinterpret_cast<u32x4*>(wt + (lr + 8) * kPitch + lc * 16);
+  const u32x4* rd = reinterpret_cast<const u32x4*>(wt + col * kPitch + quad * 32);
+
+  // Weight batches (native vectors: a struct copy into LDS would keep the
+  // array in scratch memory).
+  u32x4 wv[kU][S][2];
+#define HTN_ISSUE(JB)                                                                 \
+  {                                                                                  \
+    _Pragma("unroll") for (int u = 0; u < kU; ++u) {                                 \
+      int j = (JB) + u * W;                                                          \
+      j = j < j1 ? j : j1 - 1;                                                       \
+      _Pragma("unroll") for (int s = 0; s < S; ++s)                                  \
+        _Pragma("unroll") for (int h = 0; h < 2; ++h)                                \
+          wv[u][s][h] = *reinterpret_cast<const u32x4*>(wrow[s][h] + j * kStep);     \
+    }                                                                                \
+  }
+  HTN_ISSUE(j0 + wave);
 
   f32x4_t acc[MT][S];
 #pragma unroll
@@ -118,8 +135,23 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
     for (int s = 0; s < S; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int jb = j0 + wave; jb < j1; jb += W * kU) {
-    if (jb != j0 + wave) issue(jb);
-    uint4 av[kU][MT][2];
+    // Each 16-row x 64-element tile goes through this wave's LDS tile. LDS
+    // operations of one wave execute in issue order: the reads see the
+    // writes, and the next tile's writes follow the previous reads.
+    u32x4 bf[kU][S][2];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        *wr0 = wv[u][s][0];
+        *wr1 = wv[u][s][1];
+        __builtin_amdgcn_wave_barrier();
+        bf[u][s][0] = rd[0];
+        bf[u][s][1] = rd[1];
+        __builtin_amdgcn_wave_barrier();
+      }
+    // The next batch is in flight during this batch's multiplies.
+    if (jb + W * kU < j1) HTN_ISSUE(jb + W * kU);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int j = jb + u * W;
@@ -127,22 +159,21 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
       const int k = (ok ? j : j1 - 1) * kStep + quad * 16;
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        av[u][t][0] = a_fragment(a, t * 16 + col, k, ok);
-        av[u][t][1] = a_fragment(a, t * 16 + col, k + 8, ok);
+        const uint4 a0 = a_fragment(a, t * 16 + col, k, ok);
+        const uint4 a1 = a_fragment(a, t * 16 + col, k + 8, ok);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, a0), __builtin_bit_cast(bf16x8_t, bf[u][s][0]),
+              acc[t][s], 0, 0, 0);
+          acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, a1), __builtin_bit_cast(bf16x8_t, bf[u][s][1]),
+              acc[t][s], 0, 0, 0);
+        }
       }
     }
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-          for (int s = 0; s < S; ++s)
-            acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8_t, av[u][t][h]),
-                __builtin_bit_cast(bf16x8_t, wv[u][s][h]), acc[t][s], 0, 0, 0);
   }
+#undef HTN_ISSUE
 
   // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + i.
 #pragma unroll
