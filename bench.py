@@ -51,6 +51,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from hackthenorth_amd import _lib  # noqa: E402
 from hackthenorth_amd import decode as D  # noqa: E402
 from hackthenorth_amd.kernels import projection as P  # noqa: E402
 from hackthenorth_amd.kernels import rng as DR  # noqa: E402
@@ -340,6 +341,25 @@ def copy_peak(nbytes=2 << 30, reps=5):
     return 2 * nbytes / sec / 1e9
 
 
+def read_peak(nbytes=2 << 30, reps=5):
+    """Streaming-read bandwidth (htn_stream_read over nbytes, GB/s): the
+    practical ceiling of read-dominated kernels such as the GEMVs."""
+    src = DR.normal_(torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda"), 9, 9, 1.0)
+    out = torch.empty(int(_lib.load().htn_stream_read_blocks()), dtype=torch.int32, device="cuda")
+    st = _lib.stream()
+    _lib.call("htn_stream_read", _lib.ptr(src), nbytes, _lib.ptr(out), st)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        _lib.call("htn_stream_read", _lib.ptr(src), nbytes, _lib.ptr(out), st)
+    end.record()
+    end.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / reps
+    del src, out
+    return nbytes / sec / 1e9
+
+
 def per_op_microbench(reps=10, latency_launches=200):
     """The row-wise fused ops at Qwen3-0.6B widths (bf16 activations N(0,1)):
     bandwidth over 32768 rows (algorithmic bytes / average launch time; the
@@ -590,7 +610,8 @@ def main():
     dom = dominant_kernel(res["model"])
     log(f"dominant kernel: {dom['avg_us']:.2f} us/launch, {dom['achieved']:.0f} GB/s")
     copy_gbs = copy_peak()
-    log(f"device copy: {copy_gbs:.0f} GB/s")
+    read_gbs = read_peak()
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + write), streaming read: {read_gbs:.0f} GB/s")
     trace_us = trace_average_us(dom["instance"])
     line = {
         "metric": METRIC, "value": round(res["tok_s"], 2), "unit": "tok/s", "n_gpus": 1,
@@ -616,12 +637,16 @@ def main():
                      "trace_frac": (round(dom["bytes"] / trace_us / 1e3 / HBM_PEAK_GBS, 4)
                                     if trace_us else None),
                      "copy_peak_GBs": round(copy_gbs, 1),
-                     "frac_of_copy_peak": round(dom["achieved"] / copy_gbs, 4)},
+                     "frac_of_copy_peak": round(dom["achieved"] / copy_gbs, 4),
+                     "read_peak_GBs": round(read_gbs, 1),
+                     "frac_of_read_peak": round(dom["achieved"] / read_gbs, 4)},
         "decode_roofline": {"bytes_per_token": res["bytes_per_token"],
                             "achieved_GBs": round(res["bytes_per_token"] * res["tok_s"] / 1e9, 1),
                             "frac": round(res["decode_frac"], 4),
                             "frac_of_copy_peak": round(
                                 res["bytes_per_token"] * res["tok_s"] / 1e9 / copy_gbs, 4),
+                            "frac_of_read_peak": round(
+                                res["bytes_per_token"] * res["tok_s"] / 1e9 / read_gbs, 4),
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / res["bytes_per_token"], 1)},
         "prefill_s": round(res["prefill_s"], 3),
         "first_tokens": [res["first"]] + res["tokens"][:15],

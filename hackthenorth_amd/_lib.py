@@ -57,6 +57,8 @@ SIGNATURES = {
                                     _P, _P, _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],
     "htn_gate_up_swiglu_scratch_bytes": [_I64, _I64, _I64],
+    "htn_stream_read_blocks": [],
+    "htn_stream_read": [_P, _I64, _P, _P],
     "htn_gate_up_swiglu": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P],
     "htn_norm_rope_cache": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _F, _F,
                             _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _P, _P, _I64, _I64,
@@ -73,7 +75,7 @@ SIGNATURES = {
     "htn_attention_merge_in_kernel": [],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
-            "htn_gate_up_swiglu_scratch_bytes": _I64,
+            "htn_gate_up_swiglu_scratch_bytes": _I64, "htn_stream_read_blocks": _I64,
             "htn_head_scratch_capacity": _I64}
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX, EPI_RESIDUAL_NORM = 0, 1, 2, 3, 4
 

@@ -219,6 +219,40 @@ __global__ __launch_bounds__(kBlock) void embed_scalar(const int64_t* __restrict
     out[t * hidden + c] = ok ? table[id * hidden + c] : static_cast<bf16_t>(0);
 }
 
+// Streaming read of `vecs` 16-byte vectors (the HBM read ceiling that the
+// GEMVs are measured against): each wave reads consecutive 4 KB pieces (four
+// 1 KB non-temporal loads in flight, lane-contiguous), two blocks per CU,
+// folded with XOR into one word per block so the loads cannot be dropped.
+// Of the grid-stride and per-wave-piece patterns with 4-16 loads in flight
+// and 2-16 blocks per CU this one streamed fastest over 2 GB.
+__global__ __launch_bounds__(kBlock) void stream_read(const uint4* __restrict__ src, long vecs,
+                                                      uint32_t* __restrict__ out) {
+  constexpr int U = 4;
+  constexpr long kPiece = 64L * U;  // vectors per wave piece
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long pieces = vecs / kPiece;
+  const long waves = static_cast<long>(gridDim.x) * (kBlock / kWave);
+  uint32_t acc = 0;
+  for (long c = static_cast<long>(blockIdx.x) * (kBlock / kWave) + wave; c < pieces; c += waves) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = load_stream16(src + c * kPiece + u * 64 + lane);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  // The last partial piece, vector by vector.
+  for (long i = pieces * kPiece + static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < vecs;
+       i += static_cast<long>(gridDim.x) * kBlock) {
+    const uint4 v = load_stream16(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  __shared__ uint32_t red[kBlock / kWave];
+  for (int m = 32; m >= 1; m >>= 1) acc ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), m, kWave));
+  if (lane == 0) red[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 namespace {
 int g_cus[64];
 }
@@ -240,6 +274,16 @@ int device_cus() {
 using namespace htn;
 
 extern "C" int htn_version(void) { return 1; }
+
+extern "C" int64_t htn_stream_read_blocks(void) { return 2L * device_cus(); }
+
+extern "C" int htn_stream_read(const void* src, int64_t bytes, uint32_t* out, htn_stream_t stream) {
+  if (!src || !out || bytes <= 0 || bytes % 16 || !aligned16(src)) return HTN_EINVAL;
+  hipLaunchKernelGGL(stream_read, dim3(2 * device_cus()), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
+                     static_cast<long>(bytes / 16), out);
+  return launch_status();
+}
 
 namespace {
 

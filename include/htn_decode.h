@@ -251,6 +251,14 @@ int htn_gate_up_swiglu(const void* x, int64_t x_stride, const void* w, int64_t w
                        int64_t rows, void* y, int64_t y_stride, void* scratch,
                        htn_stream_t stream);
 
+/* Measurement helper with no reference counterpart: reads `bytes` (a
+ * multiple of 16, 16-byte aligned) of src once with streaming 16-byte loads
+ * and writes one XOR-folded word per block to out[0 .. htn_stream_read_blocks()),
+ * so that benchmarks can quote a kernel's bandwidth against the measured
+ * streaming-read ceiling beside the nominal HBM peak. */
+int64_t htn_stream_read_blocks(void);
+int htn_stream_read(const void* src, int64_t bytes, uint32_t* out, htn_stream_t stream);
+
 /* out[r] = argmax over bf16 logits[r, :n] (lowest id on ties) for r < rows. */
 int htn_argmax_bf16(const void* logits, int64_t rows, int64_t n, int64_t* out,
                     htn_stream_t stream);

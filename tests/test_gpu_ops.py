@@ -447,3 +447,19 @@ def test_captured_graph_replays_track_changed_inputs():
         values.copy_(vb)
         eager = run()
         assert bits_equal(got, eager.cpu())
+
+
+@pytest.mark.parametrize("nbytes", [16, 16 * 1000, 16 * (256 * 7) + 48, 64 << 20])
+def test_stream_read_folds_every_word(nbytes):
+    """The streaming-read measurement kernel reads each 16-byte vector once:
+    the XOR of its per-block words equals the XOR of every input word (sizes
+    with a partial last piece included)."""
+    gen = torch.Generator().manual_seed(nbytes)
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, generator=gen)
+    out = torch.full((int(_lib.load().htn_stream_read_blocks()),), 7, dtype=torch.int32,
+                     device="cuda")
+    src = words.cuda()
+    _lib.call("htn_stream_read", _lib.ptr(src), nbytes, _lib.ptr(out), _lib.stream())
+    expected = np.bitwise_xor.reduce(words.numpy().view(np.uint32))
+    got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+    assert got == expected
