@@ -55,7 +55,11 @@ struct RowsArgs {
   // normed [M][N] = bf16(gain * bf16(y * inv)), the row-wise RMSNorm of y.
   const bf16_t* ngain; float neps;
   bf16_t* normed;
+  // RMSNorm of the input rows inside the projection (NORM kernels).
+  const bf16_t* xgain; float xeps;
 };
+
+constexpr int kNormVec = 16;  // 16-byte vectors per lane of a row normalised in-kernel (K <= 8192)
 
 constexpr long kAlign = 256;
 long align_up(long v) { return (v + kAlign - 1) / kAlign * kAlign; }
@@ -83,12 +87,17 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, int m, int n, float
 
 constexpr int kPitch = 144;  // bytes per staged 64-element weight row (+16: conflict-free reads)
 
-template <int MT, int S, int EPI, int W>
+template <int MT, int S, int EPI, int W, bool NORM>
 __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   __shared__ float red[W][MT][S][kStrip * 16];
   __shared__ uint64_t best[kMaxRowsMT][kStrip];
   __shared__ __align__(16) unsigned char tile[W][16 * kPitch];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float inv_s[NORM ? kMaxRowsMT : 1];
+  const int tid = threadIdx.x, lane = tid & 63;
+  // The wave index is uniform: readfirstlane keeps step indices and buffer
+  // descriptors in scalar registers (a descriptor the compiler thinks varies
+  // per lane is applied through a loop over lanes).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int strip = blockIdx.x, ks = blockIdx.y;
   const int n0 = strip * kStrip;
   const int col = lane & 15, quad = lane >> 4;
@@ -98,16 +107,20 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   const int j1 = j0 + a.steps_per_split < total_steps ? j0 + a.steps_per_split : total_steps;
 
   // Load mapping: lane l reads 16 bytes (chunk l & 7) of strip rows l >> 3
-  // and (l >> 3) + 8, clamped to the last row (extra columns are discarded).
+  // and (l >> 3) + 8, through a buffer descriptor over the strip's rows:
+  // rows past N (last strip) read zeros, and a batch past the wave's last
+  // step gets an empty descriptor, so the loads need neither clamping nor a
+  // branch (a branch that joins with fewer loads in flight makes the
+  // compiler wait for all of them).
   const int lr = lane >> 3, lc = lane & 7;
-  const bf16_t* wrow[S][2];
+  const uint32_t strip_bytes =
+      static_cast<uint32_t>(a.N - n0 < kStrip ? a.N - n0 : kStrip) * static_cast<uint32_t>(a.K) * 2u;
+  const unsigned char* sbase[S];
 #pragma unroll
   for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int n = n0 + lr + 8 * h < a.N ? n0 + lr + 8 * h : a.N - 1;
-      wrow[s][h] = a.w + static_cast<long>(n + s * a.N) * a.K + lc * 8;
-    }
+    sbase[s] = reinterpret_cast<const unsigned char*>(a.w + static_cast<long>(n0 + s * a.N) * a.K);
+  const uint32_t voff0 = (static_cast<uint32_t>(lr) * a.K + lc * 8) * 2u;
+  const uint32_t voff1 = voff0 + 8u * static_cast<uint32_t>(a.K) * 2u;
   unsigned char* wt = tile[wave];
   u32x4* wr0 = reinterpret_cast<u32x4*>(wt + lr * kPitch + lc * 16);
   u32x4* wr1 = reinterpret_cast<u32x4*>(wt + (lr + 8) * kPitch + lc * 16);
@@ -116,17 +129,83 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   // Weight batches (native vectors: a struct copy into LDS would keep the
   // array in scratch memory).
   u32x4 wv[kU][S][2];
-#define HTN_ISSUE(JB)                                                                 \
-  {                                                                                  \
-    _Pragma("unroll") for (int u = 0; u < kU; ++u) {                                 \
-      int j = (JB) + u * W;                                                          \
-      j = j < j1 ? j : j1 - 1;                                                       \
-      _Pragma("unroll") for (int s = 0; s < S; ++s)                                  \
-        _Pragma("unroll") for (int h = 0; h < 2; ++h)                                \
-          wv[u][s][h] = *reinterpret_cast<const u32x4*>(wrow[s][h] + j * kStep);     \
-    }                                                                                \
+#define HTN_ISSUE(JB)                                                                      \
+  {                                                                                       \
+    _Pragma("unroll") for (int u = 0; u < kU; ++u) {                                      \
+      const int j = (JB) + u * W;                                                         \
+      const uint32_t range = j < j1 ? strip_bytes : 0u;                                   \
+      const uint32_t soff = static_cast<uint32_t>(j < j1 ? j : 0) * kStep * 2u;           \
+      _Pragma("unroll") for (int s = 0; s < S; ++s) {                                     \
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sbase[s], range);                   \
+        wv[u][s][0] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff0, soff, 0);         \
+        wv[u][s][1] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff1, soff, 0);         \
+      }                                                                                   \
+    }                                                                                     \
+  }
+  // RMSNorm prologue (NORM): each input row's 1 / rms by one wave, in the
+  // row-norm kernel's order (lane l over vectors l, l + 64, ..., element by
+  // element, then one wave sum), so the normalised fragments below equal
+  // the row-norm kernel's output bit for bit. A wave's first row is loaded
+  // before the first weight batch: vector loads complete in issue order, so
+  // the reduction waits only for the row, with the weights still in flight.
+  // Registers: the first kNormHead vectors per lane (rows up to 4096) are
+  // held from before the weight issue; longer rows load the rest afterwards,
+  // summed in the same order.
+  constexpr int kNormHead = 8;
+  const int nv = a.K >> 3;
+  uint4 xv[NORM ? kNormHead : 1];
+  // Row m of x through a descriptor over its K elements: vectors past the
+  // row read zeros, without a branch.
+  auto xrow = [&](int m) { return buffer_rsrc(a.x + m * a.x_rs, static_cast<uint32_t>(a.K) * 2u); };
+  if constexpr (NORM) {
+    const __amdgpu_buffer_rsrc_t rs = xrow(wave < a.M ? wave : 0);
+#pragma unroll
+    for (int jv = 0; jv < kNormHead; ++jv) xv[jv] = buffer_load16(rs, (jv * 64 + lane) * 16u, 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weights
   }
   HTN_ISSUE(j0 + wave);
+  if constexpr (NORM) {
+    // 1 / rms of row m from its first kNormHead vectors (given) and the rest
+    // (loaded here), summed in the row-norm kernel's order.
+    auto row_inv = [&](int m, const uint4 (&head)[kNormHead]) {
+      float ss = 0.f;
+#pragma unroll
+      for (int jv = 0; jv < kNormHead; ++jv) {
+        float f[8];
+        unpack8(head[jv], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+      }
+      for (int v = kNormHead * 64 + lane; v < nv; v += 64) {
+        float f[8];
+        unpack8(*reinterpret_cast<const uint4*>(a.x + m * a.x_rs + v * 8), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+      }
+      return 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.xeps);
+    };
+    // The wave's first row, preloaded (padded rows: zero fragments stay zero).
+    {
+      const float inv = wave < a.M ? row_inv(wave, xv) : 0.f;
+      if (lane == 0) inv_s[wave] = inv;
+    }
+    // Rows past the first per wave (more rows than waves).
+    for (int m = wave + W; m < kMaxRowsMT; m += W) {
+      float inv = 0.f;
+      if (m < a.M) {
+        const __amdgpu_buffer_rsrc_t rs = xrow(m);
+        uint4 more[kNormHead];
+#pragma unroll
+        for (int jv = 0; jv < kNormHead; ++jv) more[jv] = buffer_load16(rs, (jv * 64 + lane) * 16u, 0);
+        inv = row_inv(m, more);
+      }
+      if (lane == 0) inv_s[m] = inv;
+    }
+    // LDS-only barrier: __syncthreads would also wait for every vector load
+    // in flight, i.e. for the first weight batch, one memory round trip
+    // before the loop could issue the next one.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
 
   f32x4_t acc[MT][S];
 #pragma unroll
@@ -135,6 +214,25 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
     for (int s = 0; s < S; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int jb = j0 + wave; jb < j1; jb += W * kU) {
+    // This batch's A fragments (x, and the gain under NORM) first: vector
+    // loads complete in issue order, so the multiplies wait only for these,
+    // not for the next weight batch issued below.
+    uint4 av[kU][MT][2], gv[kU][NORM ? 2 : 1];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int j = jb + u * W;
+      const bool ok = j < j1;
+      const int k = (ok ? j : j1 - 1) * kStep + quad * 16;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        av[u][t][0] = a_fragment(a, t * 16 + col, k, ok);
+        av[u][t][1] = a_fragment(a, t * 16 + col, k + 8, ok);
+      }
+      if constexpr (NORM) {
+        gv[u][0] = *reinterpret_cast<const uint4*>(a.xgain + k);
+        gv[u][1] = *reinterpret_cast<const uint4*>(a.xgain + k + 8);
+      }
+    }
     // Each 16-row x 64-element tile goes through this wave's LDS tile. LDS
     // operations of one wave execute in issue order: the reads see the
     // writes, and the next tile's writes follow the previous reads.
@@ -150,28 +248,34 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
         bf[u][s][1] = rd[1];
         __builtin_amdgcn_wave_barrier();
       }
-    // The next batch is in flight during this batch's multiplies.
-    if (jb + W * kU < j1) HTN_ISSUE(jb + W * kU);
+    // The next batch (empty past the wave's last step) is in flight during
+    // this batch's normalisation and multiplies; the scheduling barrier keeps
+    // the normalisation (which waits for the fragments) after the issue.
+    HTN_ISSUE(jb + W * kU);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int j = jb + u * W;
-      const bool ok = j < j1;
-      const int k = (ok ? j : j1 - 1) * kStep + quad * 16;
+      for (int u = 0; u < kU; ++u)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const uint4 a0 = a_fragment(a, t * 16 + col, k, ok);
-        const uint4 a1 = a_fragment(a, t * 16 + col, k + 8, ok);
+        for (int t = 0; t < MT; ++t) {
+          const float inv = inv_s[t * 16 + col];
+          av[u][t][0] = norm8(av[u][t][0], gv[u][0], inv);
+          av[u][t][1] = norm8(av[u][t][1], gv[u][1], inv);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, a0), __builtin_bit_cast(bf16x8_t, bf[u][s][0]),
+              __builtin_bit_cast(bf16x8_t, av[u][t][0]), __builtin_bit_cast(bf16x8_t, bf[u][s][0]),
               acc[t][s], 0, 0, 0);
           acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, a1), __builtin_bit_cast(bf16x8_t, bf[u][s][1]),
+              __builtin_bit_cast(bf16x8_t, av[u][t][1]), __builtin_bit_cast(bf16x8_t, bf[u][s][1]),
               acc[t][s], 0, 0, 0);
         }
-      }
-    }
   }
 #undef HTN_ISSUE
 
@@ -454,10 +558,11 @@ int choose_splits(int strips, int waves, int K) {
   return ks < 1 ? 1 : ks;
 }
 
-template <int MT, int S, int EPI, int W>
+template <int MT, int S, int EPI, int W, bool NORM>
 int launch_w(RowsArgs& a, hipStream_t st) {
   const int strips = (a.N + kStrip - 1) / kStrip;
-  hipLaunchKernelGGL((gemm_rows_kernel<MT, S, EPI, W>), dim3(strips, a.KS), dim3(W * 64), 0, st, a);
+  hipLaunchKernelGGL((gemm_rows_kernel<MT, S, EPI, W, NORM>), dim3(strips, a.KS), dim3(W * 64), 0,
+                     st, a);
   if (launch_status() != HTN_OK) return HTN_ELAUNCH;
   if (EPI == HTN_EPI_ARGMAX) {
     hipLaunchKernelGGL(gemm_rows_argmax, dim3(a.M), dim3(kBlock), 0, st, a.keys, strips, a.M, a.tokens);
@@ -471,21 +576,34 @@ int launch_w(RowsArgs& a, hipStream_t st) {
   return launch_status();
 }
 
-template <int MT, int S, int EPI>
+template <int MT, int S, int EPI, bool NORM = false>
 int launch(RowsArgs& a, int waves, hipStream_t st) {
-  if (waves >= 16) return launch_w<MT, S, EPI, 16>(a, st);
-  if (waves >= 8) return launch_w<MT, S, EPI, 8>(a, st);
-  return launch_w<MT, S, EPI, 4>(a, st);
+  if (waves >= 16) return launch_w<MT, S, EPI, 16, NORM>(a, st);
+  if (waves >= 8) return launch_w<MT, S, EPI, 8, NORM>(a, st);
+  return launch_w<MT, S, EPI, 4, NORM>(a, st);
 }
 
+// `norm`: the input rows are normalised inside the projection (store and
+// SwiGLU epilogues only).
 template <int MT>
-int dispatch_epi(RowsArgs& a, int epi, int waves, hipStream_t st) {
+int dispatch_epi(RowsArgs& a, int epi, bool norm, int waves, hipStream_t st) {
   switch (epi) {
-    case HTN_EPI_STORE: return launch<MT, 1, HTN_EPI_STORE>(a, waves, st);
+    case HTN_EPI_STORE:
+      return norm ? launch<MT, 1, HTN_EPI_STORE, true>(a, waves, st)
+                  : launch<MT, 1, HTN_EPI_STORE>(a, waves, st);
     case HTN_EPI_RESIDUAL: return launch<MT, 1, HTN_EPI_RESIDUAL>(a, waves, st);
-    case HTN_EPI_SWIGLU: return launch<MT, 2, HTN_EPI_SWIGLU>(a, waves, st);
+    case HTN_EPI_SWIGLU:
+      return norm ? launch<MT, 2, HTN_EPI_SWIGLU, true>(a, waves, st)
+                  : launch<MT, 2, HTN_EPI_SWIGLU>(a, waves, st);
     default: return launch<MT, 1, HTN_EPI_ARGMAX>(a, waves, st);
   }
+}
+
+// Input RMSNorm inside the projection: store and SwiGLU epilogues, rows of at
+// most kNormVec * 512 elements. The greedy head keeps the one-launch
+// pre-pass: its thousands of strips would each re-read every row.
+bool norm_in_kernel(int epilogue, long k) {
+  return (epilogue == HTN_EPI_STORE || epilogue == HTN_EPI_SWIGLU) && k <= kNormVec * 512;
 }
 
 struct Plan {
@@ -498,7 +616,7 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
   const int strips = static_cast<int>((N + kStrip - 1) / kStrip);
   p.waves = choose_waves(strips, static_cast<int>(K));
   p.ks = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, p.waves, static_cast<int>(K));
-  p.norm_bytes = norm ? align_up(M * K * 2) : 0;
+  p.norm_bytes = norm && !norm_in_kernel(epilogue, K) ? align_up(M * K * 2) : 0;
   if (epilogue == HTN_EPI_ARGMAX) p.tail_bytes = static_cast<long>(strips) * M * 8;
   else if (p.ks > 1) p.tail_bytes = static_cast<long>(p.ks) * M * N * (epilogue == HTN_EPI_SWIGLU ? 2 : 1) * 4;
   return p;
@@ -589,7 +707,11 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   RowsArgs a{};
   a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
-  if (gain) {
+  const bool inorm = gain && norm_in_kernel(epilogue, k);
+  if (inorm) {
+    a.xgain = static_cast<const bf16_t*>(gain);
+    a.xeps = eps;
+  } else if (gain) {
     // Rows normalised once into the scratch buffer.
     bf16_t* xn = static_cast<bf16_t*>(scratch);
     const int rc = htn_rms_norm(x, x_stride, gain, xn, rows, k, eps, stream);
@@ -608,8 +730,8 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   a.part = static_cast<float*>(tail);
   a.keys = static_cast<uint64_t*>(tail);
   a.tokens = tokens;
-  if (rows <= 16) return dispatch_epi<1>(a, epilogue, p.waves, st);
-  return dispatch_epi<2>(a, epilogue, p.waves, st);
+  if (rows <= 16) return dispatch_epi<1>(a, epilogue, inorm, p.waves, st);
+  return dispatch_epi<2>(a, epilogue, inorm, p.waves, st);
 }
 
 extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w,

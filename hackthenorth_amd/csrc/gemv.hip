@@ -179,20 +179,6 @@ __device__ __forceinline__ void issue_epilogue(const GemvArgs& a, long n0, float
 // elements (8192): each thread loads its x and gain vectors once.
 constexpr int kNormVecs = 4;
 
-// bf16(g * bf16(x * inv)) for eight packed elements (the reference's RMSNorm
-// roundings).
-__device__ __forceinline__ uint4 norm8(uint4 xv, uint4 gv, float inv) {
-  float f[8], g[8];
-  unpack8(xv, f);
-  unpack8(gv, g);
-  uint4 o;
-  o.x = pack_bf2(g[0] * round_bf(f[0] * inv), g[1] * round_bf(f[1] * inv));
-  o.y = pack_bf2(g[2] * round_bf(f[2] * inv), g[3] * round_bf(f[3] * inv));
-  o.z = pack_bf2(g[4] * round_bf(f[4] * inv), g[5] * round_bf(f[5] * inv));
-  o.w = pack_bf2(g[6] * round_bf(f[6] * inv), g[7] * round_bf(f[7] * inv));
-  return o;
-}
-
 __device__ __forceinline__ void pin4(uint4& v) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }

@@ -22,7 +22,8 @@ from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
-from .kernels.rows import greedy_rows, projection_rows, residual_norm_rows, swiglu_rows
+from .kernels.rows import (greedy_rows, projection_rows, residual_norm_rows, residual_rows,
+                           splits_k, swiglu_rows)
 from .speculate import draft_width, verified_tokens
 
 
@@ -188,12 +189,22 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                                   positions)
         a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
         if multi:
-            r, rn = residual_norm_rows(a, layer.o_weight, h, ln2.weight, ln2.variance_epsilon)
-            m = swiglu_rows(rn, layer.gate_up_weight)
+            # A projection that splits K writes the next RMSNorm in its split
+            # finish; otherwise the next projection normalises its rows itself.
+            if splits_k(*layer.o_weight.shape):
+                r, rn = residual_norm_rows(a, layer.o_weight, h, ln2.weight,
+                                           ln2.variance_epsilon)
+                m = swiglu_rows(rn, layer.gate_up_weight)
+            else:
+                r = residual_rows(a, layer.o_weight, h)
+                m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
             nxt = model.layers[i + 1].input_layernorm if i + 1 < len(model.layers) \
                 else model.norm
-            h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,
-                                       nxt.variance_epsilon)
+            if splits_k(*layer.down_weight.shape):
+                h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,
+                                           nxt.variance_epsilon)
+            else:
+                h, hn = residual_rows(m, layer.down_weight, r), None
         else:
             r = torch.stack([output_projection_residual(a[j], layer.o_weight, h[j])
                              for j in range(rows)])
@@ -205,11 +216,16 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
             record.append(h.view(b, t, hidden))
     kept = 1 if last_only else t
     if multi:
-        # hn is the final RMSNorm of h (the last down projection fused it).
-        xn = hn.view(b, t, hidden)
-        xn = xn[:, -1:] if last_only else xn
-        return greedy_rows(xn.reshape(-1, hidden).contiguous(),
-                           model.lm_head_weight).view(b, kept)
+        if hn is not None:
+            # hn is the final RMSNorm of h (the last down projection fused it).
+            xn = hn.view(b, t, hidden)
+            xn = xn[:, -1:] if last_only else xn
+            return greedy_rows(xn.reshape(-1, hidden).contiguous(),
+                               model.lm_head_weight).view(b, kept)
+        x = h.view(b, t, hidden)
+        x = x[:, -1:] if last_only else x
+        return greedy_rows(x.reshape(-1, hidden).contiguous(), model.lm_head_weight,
+                           model.norm.weight, model.norm.variance_epsilon).view(b, kept)
     x = h.view(b, t, hidden)
     flat = (x[:, -1:] if last_only else x).reshape(-1, hidden).contiguous()
     out = torch.empty((flat.shape[0],), dtype=torch.int64, device=model.device)

@@ -67,6 +67,13 @@ def residual_rows(x, weight, residual):
     return out
 
 
+def splits_k(n, k):
+    """Whether the multi-row projection of a [n, k] weight splits K across
+    blocks (the plan depends on the weight shape only, not on the rows): its
+    split finish can then also write the next RMSNorm at no extra launch."""
+    return _lib.load().htn_gemm_rows_scratch_bytes(1, n, k, _lib.EPI_RESIDUAL, 0) > 0
+
+
 def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
     """(out, normed): out = residual_rows(x, weight, residual) and normed its
     RMSNorm with `gain` (the next layer's input), both written by one launch

@@ -82,6 +82,20 @@ def test_greedy_rows_match_oracle_argmax(m):
             assert float(logits[r, expected] - logits[r, got]) < 1e-3, (r, got, expected)
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 1024, 2560), (8, 9728, 2560), (17, 512, 4096),
+                                   (32, 256, 8192), (3, 100, 64)])
+def test_in_kernel_norm_equals_row_norm_then_projection(m, n, k):
+    """Projections with a gain normalise their rows inside the kernel (store
+    and SwiGLU epilogues, K <= 8192), in the row-norm kernel's summation
+    order: bit-identical to rms_norm followed by the plain projection."""
+    w = nrm(50, (2 * n, k), std=0.02).cuda()
+    x, g = nrm(51, (m, k)).cuda(), nrm(52, (k,)).cuda()
+    normed = rms_norm(x, g, 1e-6)
+    top = w[:n].contiguous()
+    assert torch.equal(RW.projection_rows(x, top, g, 1e-6), RW.projection_rows(normed, top))
+    assert torch.equal(RW.swiglu_rows(x, w, g, 1e-6), RW.swiglu_rows(normed, w))
+
+
 def test_greedy_rows_ties_choose_lowest_id():
     v, k = 151936, 1024
     w = torch.zeros(v, k, dtype=torch.bfloat16, device="cuda")
