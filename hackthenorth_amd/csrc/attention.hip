@@ -2027,11 +2027,14 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
   if (a.Q == 1 && rows <= 8 && heads <= 8 && tiles <= 144) {
     // Up to 8 (batch, kv head) pairs and 9K slots (measured, 2 and 4 query
     // rows per kv head, 512 to 8192 slots): one tile per block up to 24
-    // tiles, then two, then three (fewer splits leave the in-kernel merge
-    // less to read; four or more need the 128 KB ring, one block per CU).
-    // Four or more query rows per kv head score and weigh on the matrix
-    // cores; two rows are faster on the vector unit.
-    const long nt = tiles <= 24 ? 1 : (tiles <= 40 ? 2 : 3);
+    // tiles, then two, then three up to 80 tiles (fewer splits leave the
+    // in-kernel merge less to read), then six: past ~80 tiles three-tile
+    // splits outnumber the CUs and the blocks sharing a CU finish last,
+    // while six keep one block per CU (8B at 6144 and 8192 slots: about
+    // 1.3 us less per layer; a ring of four tiles, one 128 KB block per CU,
+    // was slower). Four or more query rows per kv head score and weigh on
+    // the matrix cores; two rows are faster on the vector unit.
+    const long nt = tiles <= 24 ? 1 : (tiles <= 40 ? 2 : (tiles <= 80 ? 3 : 6));
     a.ring = nt == 1 ? 1 : 2;
     a.mfma = rows >= 3;
     split = nt * kSplit;
