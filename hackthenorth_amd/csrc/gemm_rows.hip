@@ -1,8 +1,9 @@
-// Multi-row projections for the speculative verify pass (2 to 32 rows).
+// Multi-row projections: verify passes, batched decode steps and prefill
+// chunks (2 to 128 rows).
 //
 // y[m, n] = sum_k x[m, k] W[n, k] for every row m < M with the weight read
 // once for all rows: the rows form the A operand of gfx950's
-// v_mfma_f32_16x16x32_bf16 (one or two 16-row tiles, rows past M are zero),
+// v_mfma_f32_16x16x32_bf16 (one to eight 16-row tiles, rows past M are zero),
 // a strip of 16 weight rows the B operand. The kernel stays HBM-bound on W:
 //
 //  * block = W waves (4 to 16, more when strips are few) on one 16-column
@@ -37,7 +38,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kStrip = 16;     // output columns per block (MFMA N)
 constexpr int kStep = 64;      // k per step: two MFMAs of 32
-constexpr int kMaxRowsMT = 32; // two 16-row tiles
+constexpr int kMaxRowsMT = 128; // eight 16-row tiles (prefill chunks, large batches)
+constexpr int kMaxRowsI = 32;   // rows per launch of the interleaved gate/up kernel
 constexpr int kU = 1;          // k steps per wave per batch (1 measured fastest of 1, 2, 4)
 constexpr int kMaxWaves = 16;
 constexpr int kMaxK = 16384;
@@ -90,9 +92,9 @@ constexpr int kPitch = 144;  // bytes per staged 64-element weight row (+16: con
 template <int MT, int S, int EPI, int W, bool NORM>
 __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
   __shared__ float red[W][MT][S][kStrip * 16];
-  __shared__ uint64_t best[kMaxRowsMT][kStrip];
+  __shared__ uint64_t best[EPI == HTN_EPI_ARGMAX ? MT * 16 : 1][kStrip];
   __shared__ __align__(16) unsigned char tile[W][16 * kPitch];
-  __shared__ float inv_s[NORM ? kMaxRowsMT : 1];
+  __shared__ float inv_s[NORM ? MT * 16 : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   // The wave index is uniform: readfirstlane keeps step indices and buffer
   // descriptors in scalar registers (a descriptor the compiler thinks varies
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
       if (lane == 0) inv_s[wave] = inv;
     }
     // Rows past the first per wave (more rows than waves).
-    for (int m = wave + W; m < kMaxRowsMT; m += W) {
+    for (int m = wave + W; m < MT * 16; m += W) {
       float inv = 0.f;
       if (m < a.M) {
         const __amdgpu_buffer_rsrc_t rs = xrow(m);
@@ -576,10 +578,18 @@ int launch_w(RowsArgs& a, hipStream_t st) {
   return launch_status();
 }
 
+// Most waves per block for MT row tiles: the per-wave reduction array
+// (W * MT * S KB of LDS) stays within 64 KB.
+constexpr int max_waves(int mt) { return mt <= 2 ? 16 : (mt == 4 ? 8 : 4); }
+
 template <int MT, int S, int EPI, bool NORM = false>
 int launch(RowsArgs& a, int waves, hipStream_t st) {
-  if (waves >= 16) return launch_w<MT, S, EPI, 16, NORM>(a, st);
-  if (waves >= 8) return launch_w<MT, S, EPI, 8, NORM>(a, st);
+  if constexpr (max_waves(MT) >= 16) {
+    if (waves >= 16) return launch_w<MT, S, EPI, 16, NORM>(a, st);
+  }
+  if constexpr (max_waves(MT) >= 8) {
+    if (waves >= 8) return launch_w<MT, S, EPI, 8, NORM>(a, st);
+  }
   return launch_w<MT, S, EPI, 4, NORM>(a, st);
 }
 
@@ -587,23 +597,28 @@ int launch(RowsArgs& a, int waves, hipStream_t st) {
 // SwiGLU epilogues only).
 template <int MT>
 int dispatch_epi(RowsArgs& a, int epi, bool norm, int waves, hipStream_t st) {
+  if constexpr (MT <= 2) {  // the in-kernel norm covers at most 32 rows
+    if (norm && epi == HTN_EPI_STORE) return launch<MT, 1, HTN_EPI_STORE, true>(a, waves, st);
+    if (norm && epi == HTN_EPI_SWIGLU) return launch<MT, 2, HTN_EPI_SWIGLU, true>(a, waves, st);
+  }
   switch (epi) {
-    case HTN_EPI_STORE:
-      return norm ? launch<MT, 1, HTN_EPI_STORE, true>(a, waves, st)
-                  : launch<MT, 1, HTN_EPI_STORE>(a, waves, st);
+    case HTN_EPI_STORE: return launch<MT, 1, HTN_EPI_STORE>(a, waves, st);
     case HTN_EPI_RESIDUAL: return launch<MT, 1, HTN_EPI_RESIDUAL>(a, waves, st);
-    case HTN_EPI_SWIGLU:
-      return norm ? launch<MT, 2, HTN_EPI_SWIGLU, true>(a, waves, st)
-                  : launch<MT, 2, HTN_EPI_SWIGLU>(a, waves, st);
+    case HTN_EPI_SWIGLU: return launch<MT, 2, HTN_EPI_SWIGLU>(a, waves, st);
     default: return launch<MT, 1, HTN_EPI_ARGMAX>(a, waves, st);
   }
 }
 
-// Input RMSNorm inside the projection: store and SwiGLU epilogues, rows of at
-// most kNormVec * 512 elements. The greedy head keeps the one-launch
-// pre-pass: its thousands of strips would each re-read every row.
-bool norm_in_kernel(int epilogue, long k) {
-  return (epilogue == HTN_EPI_STORE || epilogue == HTN_EPI_SWIGLU) && k <= kNormVec * 512;
+// Row tiles per block for `rows` activation rows.
+int row_tiles(long rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : (rows <= 64 ? 4 : 8)); }
+
+// Input RMSNorm inside the projection: store and SwiGLU epilogues, at most 32
+// rows (one or two per wave) of at most kNormVec * 512 elements. The greedy
+// head keeps the one-launch pre-pass: its thousands of strips would each
+// re-read every row.
+bool norm_in_kernel(int epilogue, long rows, long k) {
+  return (epilogue == HTN_EPI_STORE || epilogue == HTN_EPI_SWIGLU) && rows <= 32 &&
+         k <= kNormVec * 512;
 }
 
 struct Plan {
@@ -615,8 +630,10 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
   Plan p{};
   const int strips = static_cast<int>((N + kStrip - 1) / kStrip);
   p.waves = choose_waves(strips, static_cast<int>(K));
+  const int mt = row_tiles(M);
+  if (p.waves > max_waves(mt)) p.waves = max_waves(mt);
   p.ks = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, p.waves, static_cast<int>(K));
-  p.norm_bytes = norm && !norm_in_kernel(epilogue, K) ? align_up(M * K * 2) : 0;
+  p.norm_bytes = norm && !norm_in_kernel(epilogue, M, K) ? align_up(M * K * 2) : 0;
   if (epilogue == HTN_EPI_ARGMAX) p.tail_bytes = static_cast<long>(strips) * M * 8;
   else if (p.ks > 1) p.tail_bytes = static_cast<long>(p.ks) * M * N * (epilogue == HTN_EPI_SWIGLU ? 2 : 1) * 4;
   return p;
@@ -707,7 +724,7 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   RowsArgs a{};
   a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
-  const bool inorm = gain && norm_in_kernel(epilogue, k);
+  const bool inorm = gain && norm_in_kernel(epilogue, rows, k);
   if (inorm) {
     a.xgain = static_cast<const bf16_t*>(gain);
     a.xeps = eps;
@@ -730,8 +747,12 @@ extern "C" int htn_gemm_rows(const void* x, int64_t x_stride, const void* gain, 
   a.part = static_cast<float*>(tail);
   a.keys = static_cast<uint64_t*>(tail);
   a.tokens = tokens;
-  if (rows <= 16) return dispatch_epi<1>(a, epilogue, inorm, p.waves, st);
-  return dispatch_epi<2>(a, epilogue, inorm, p.waves, st);
+  switch (row_tiles(rows)) {
+    case 1: return dispatch_epi<1>(a, epilogue, inorm, p.waves, st);
+    case 2: return dispatch_epi<2>(a, epilogue, inorm, p.waves, st);
+    case 4: return dispatch_epi<4>(a, epilogue, inorm, p.waves, st);
+    default: return dispatch_epi<8>(a, epilogue, inorm, p.waves, st);
+  }
 }
 
 extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w,
@@ -773,19 +794,23 @@ extern "C" int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, cons
   a.ngain = static_cast<const bf16_t*>(gain);
   a.neps = eps;
   a.normed = static_cast<bf16_t*>(normed);
-  if (rows <= 16) return launch<1, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
-  return launch<2, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+  switch (row_tiles(rows)) {
+    case 1: return launch<1, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+    case 2: return launch<2, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+    case 4: return launch<4, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+    default: return launch<8, 1, HTN_EPI_RESIDUAL>(a, p.waves, st);
+  }
 }
 
 extern "C" int64_t htn_gate_up_swiglu_scratch_bytes(int64_t rows, int64_t width, int64_t k) {
-  if (rows <= 0 || rows > kMaxRowsMT || width <= 0 || width % 2 || k <= 0 || k % kStepI) return 0;
+  if (rows <= 0 || rows > kMaxRowsI || width <= 0 || width % 2 || k <= 0 || k % kStepI) return 0;
   return plan_interleaved(rows, width, k).tail_bytes;
 }
 
 extern "C" int htn_gate_up_swiglu(const void* x, int64_t x_stride, const void* w, int64_t width,
                                   int64_t k, int64_t rows, void* y, int64_t y_stride,
                                   void* scratch, htn_stream_t stream) {
-  if (!x || !w || !y || rows <= 0 || rows > kMaxRowsMT || width <= 0 || k <= 0 ||
+  if (!x || !w || !y || rows <= 0 || rows > kMaxRowsI || width <= 0 || k <= 0 ||
       width > (1L << 30) || y_stride < width)
     return HTN_EINVAL;
   // 16-byte rows of x, 8-byte (gate, up) pairs of w; every step 32 rows of w.

@@ -191,7 +191,7 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
         if multi:
             # A projection that splits K writes the next RMSNorm in its split
             # finish; otherwise the next projection normalises its rows itself.
-            if splits_k(*layer.o_weight.shape):
+            if splits_k(*layer.o_weight.shape, rows):
                 r, rn = residual_norm_rows(a, layer.o_weight, h, ln2.weight,
                                            ln2.variance_epsilon)
                 m = swiglu_rows(rn, layer.gate_up_weight)
@@ -200,7 +200,7 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                 m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
             nxt = model.layers[i + 1].input_layernorm if i + 1 < len(model.layers) \
                 else model.norm
-            if splits_k(*layer.down_weight.shape):
+            if splits_k(*layer.down_weight.shape, rows):
                 h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,
                                            nxt.variance_epsilon)
             else:

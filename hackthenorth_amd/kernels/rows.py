@@ -1,17 +1,17 @@
-"""Projections of 2 to 32 rows that read each weight once (MFMA tiles).
+"""Projections of 2 to 128 rows that read each weight once (MFMA tiles).
 
 The speculative verify pass scores k + 1 tokens in one forward; the reference
 runs its multi-row projections as Triton GEMM tiles (dryft/engine/
 projections.py:168-183, kernels/gateup.py:40-58, kernels/split_down.py:85-101).
 Here every multi-row projection is one htn_gemm_rows launch (plus a K-split
 reduction when the strips alone cannot fill the GPU) with the batch-one
-GEMVs' bf16 rounding boundaries. Larger row counts run in chunks of 32.
+GEMVs' bf16 rounding boundaries. Larger row counts run in chunks of 128.
 """
 import torch
 
 from .. import _lib
 
-MAX_ROWS = 32
+MAX_ROWS = 128
 
 
 def _scratch(device, rows, n, k, epilogue, norm):
@@ -67,11 +67,12 @@ def residual_rows(x, weight, residual):
     return out
 
 
-def splits_k(n, k):
-    """Whether the multi-row projection of a [n, k] weight splits K across
-    blocks (the plan depends on the weight shape only, not on the rows): its
-    split finish can then also write the next RMSNorm at no extra launch."""
-    return _lib.load().htn_gemm_rows_scratch_bytes(1, n, k, _lib.EPI_RESIDUAL, 0) > 0
+def splits_k(n, k, rows):
+    """Whether the multi-row projection of a [n, k] weight over `rows` rows
+    (per launch: at most MAX_ROWS) splits K across blocks: its split finish
+    can then also write the next RMSNorm at no extra launch."""
+    rows = max(1, min(rows, MAX_ROWS))
+    return _lib.load().htn_gemm_rows_scratch_bytes(rows, n, k, _lib.EPI_RESIDUAL, 0) > 0
 
 
 def residual_norm_rows(x, weight, residual, gain, eps=1e-6):

@@ -196,8 +196,8 @@ int htn_lm_head_argmax_w8(const void* x, const void* gain, float eps, const void
                           int64_t* token_out, int64_t* position_inc, void* scratch,
                           htn_stream_t stream);
 
-/* ---------------------------------------------------------------- 2..32 rows
- * Projection of `rows` (1..32) activation rows x[m, :k] (row stride
+/* ---------------------------------------------------------------- 2..128 rows
+ * Projection of `rows` (1..128) activation rows x[m, :k] (row stride
  * x_stride elements) by a row-major bf16 weight w[n, k] (2n rows, gate then
  * up, for HTN_EPI_SWIGLU), reading the weight once for all rows (MFMA tiles).
  * gain != NULL applies RMSNorm to each row first:

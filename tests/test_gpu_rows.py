@@ -36,7 +36,7 @@ def within_one_ulp(actual, expected, ulps=1):
 
 
 SHAPES = [(4096, 1024), (257, 2560), (40, 4096), (100, 12288), (1536, 9728), (3, 64)]
-ROWS = [2, 5, 8, 16, 17, 32]
+ROWS = [2, 5, 8, 16, 17, 32, 33, 64, 100, 128]
 
 
 @pytest.mark.parametrize("n,k", SHAPES)
@@ -169,7 +169,8 @@ def test_split_down_residual_norm():
 
 
 @pytest.mark.parametrize("m,k,n", [(4, 9728, 2560), (20, 9728, 2560), (5, 3072, 1024),
-                                   (4, 12288, 4096), (5, 4096, 2560)])
+                                   (4, 12288, 4096), (5, 4096, 2560), (128, 9728, 2560),
+                                   (70, 12288, 4096)])
 def test_residual_norm_rows_bit_exact(m, k, n):
     """The fused entry gives the bits of the residual projection followed by
     the row-wise RMSNorm: the 9728-deep shapes split K and finish both in one
