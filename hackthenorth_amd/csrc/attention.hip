@@ -456,6 +456,52 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
   if (threadIdx.x == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The block's result per query row of the LDS-staged kernels, one wave per
+// row (r = wave, wave + 4, ...: wave-uniform, so the per-row state is read
+// by broadcast and its weights are computed once per wave): the four waves'
+// states weighted by exp2(m_w - M), M = max_w m_w, lane l holding dims 2l
+// and 2l + 1. With one split it is the output row; otherwise the split's
+// partial and its (max, sum), the max back to base e for the merge. Row r is
+// head r / Q, query r % Q of kv head kvh (one query unless MQ).
+template <int ROWS, bool MQ>
+__device__ __forceinline__ void write_rows(const AttnArgs& a, int b, int kvh, int s, int rows,
+                                           int wave, int lane, const float (*wm)[ROWS],
+                                           const float (*wl)[ROWS],
+                                           const float (*wacc)[ROWS][D]) {
+  constexpr int W = kBlock / kWave;
+  for (int r = wave; r < rows; r += W) {
+    float mw[W];
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      mw[w] = wm[w][r];
+      M = fmaxf(M, mw[w]);
+    }
+    float nx = 0.f, ny = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
+      const float2 v = *reinterpret_cast<const float2*>(&wacc[w][r][2 * lane]);
+      nx = fmaf(f, v.x, nx);
+      ny = fmaf(f, v.y, ny);
+      den = fmaf(f, wl[w][r], den);
+    }
+    const int h = kvh * a.G + (MQ ? r / a.Q : r), t = MQ ? r % a.Q : 0;
+    if (a.splits == 1) {
+      bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st + 2 * lane;
+      dst[0] = static_cast<bf16_t>(f2bf(nx / den));
+      dst[1] = static_cast<bf16_t>(f2bf(ny / den));
+    } else {
+      const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
+      *reinterpret_cast<float2*>(a.part + (orow * a.splits + s) * D + 2 * lane) =
+          make_float2(nx, ny);
+      if (lane == 0)
+        *reinterpret_cast<float2*>(a.ml + (orow * a.splits + s) * 2) =
+            make_float2(M * 0.6931471805599453f, den);
+    }
+  }
+}
+
 // Query source of the partial kernel: q rows from memory, or the fused
 // prologue over the packed projection row with the RoPE row either already
 // selected (row 0 of cos/sin) or looked up by the device position.
@@ -1302,28 +1348,7 @@ __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
     }
   }
   lds_barrier();
-  for (int i = tid; i < rows * D; i += kBlock) {
-    const int r = i / D, d = i % D;
-    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kBlock / kWave; ++w) {
-      const float f = wm[w][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][r] - M);
-      num = fmaf(f, wacc[w][r][d], num);
-      den = fmaf(f, wl[w][r], den);
-    }
-    const long orow = static_cast<long>(b) * a.Hq + kvh * a.G + r;
-    if (a.splits == 1) {
-      a.out[b * a.o_sb + (kvh * a.G + r) * a.o_sh + d] = static_cast<bf16_t>(f2bf(num / den));
-    } else {
-      a.part[(orow * a.splits + s) * D + d] = num;
-      if (d == 0) {
-        // the merge weighs partials with natural exponentials: max back to base e
-        a.ml[(orow * a.splits + s) * 2] = M * 0.6931471805599453f;
-        a.ml[(orow * a.splits + s) * 2 + 1] = den;
-      }
-    }
-  }
+  write_rows<ROWS, false>(a, b, kvh, s, rows, wave, lane, wm, wl, wacc);
   if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
@@ -1760,29 +1785,7 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
     }
   }
   lds_barrier();
-  for (int i = tid; i < rows * D; i += kBlock) {
-    const int r = i / D, d = i % D;
-    const float M = fmaxf(fmaxf(wm[0][r], wm[1][r]), fmaxf(wm[2][r], wm[3][r]));
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kBlock / kWave; ++w) {
-      const float f = wm[w][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][r] - M);
-      num = fmaf(f, wacc[w][r][d], num);
-      den = fmaf(f, wl[w][r], den);
-    }
-    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-    const long orow = (static_cast<long>(b) * a.Hq + h) * a.Q + t;
-    if (a.splits == 1) {
-      a.out[b * a.o_sb + h * a.o_sh + t * a.o_st + d] = static_cast<bf16_t>(f2bf(num / den));
-    } else {
-      a.part[(orow * a.splits + s) * D + d] = num;
-      if (d == 0) {
-        // the merge weighs partials with natural exponentials: max back to base e
-        a.ml[(orow * a.splits + s) * 2] = M * 0.6931471805599453f;
-        a.ml[(orow * a.splits + s) * 2 + 1] = den;
-      }
-    }
-  }
+  write_rows<ROWS, MQ>(a, b, kvh, s, rows, wave, lane, wm, wl, wacc);
   if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
