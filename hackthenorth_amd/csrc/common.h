@@ -215,8 +215,8 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
 // ------------------------------------------------------------------ host helpers
 
 int device_cus();  // compute units of the current device (cached per device)
-// Grid of the one-token GEMV over n rows of k weights (format 0 for bf16, or
-// HTN_WEIGHT_INT8 / HTN_WEIGHT_FP8_E4M3) without the RMSNorm prologue and without SwiGLU: its block count and
+// Grid of the one-token residual GEMV (the output projection) over n rows of k
+// weights (format 0 for bf16, or HTN_WEIGHT_INT8 / HTN_WEIGHT_FP8_E4M3): its block count and
 // the rows each block takes per grid step (block b multiplies rows
 // [b * rows, (b + 1) * rows), then the same span blocks * rows further on).
 // False when the weights take the scalar path.

@@ -454,19 +454,35 @@ int finish_argmax(const GemvArgs& a, long blocks, hipStream_t st) {
 // Waves resident per CU at full occupancy of 4 blocks (16 waves).
 constexpr long kWavesPerCu = 16;
 
+// Blocks per CU for a grid-stride GEMV over `groups` row groups (four waves
+// a block). bf16 residual projections and RMSNorm + gate/up whose row
+// groups divide evenly over the CUs take the blocks per CU that give every
+// wave the same whole number of groups, two for the residual projections
+// (each wave's second row issued while the first is reduced) and three for
+// gate/up: the 8B decode step's O, down and gate/up (4096, 4096 and 12288
+// groups on 256 CUs) measured 2.89 -> 2.85 ms per step against four, four
+// and two blocks per CU. Other shapes keep the defaults: plain and residual
+// kernels fill the CU (eight blocks); RMSNorm kernels pay their prologue
+// once per block, so two longer-lived blocks per CU beat four (measured from
+// 3072 to 151936 row groups: e.g. the 6144-row, K = 4096 QKV projection
+// takes 9.9 us at two, 10.6 us at four); 8-bit rows are half as long, so a
+// wave holds half the bytes in flight: their norm kernels keep four blocks
+// per CU (eight for 1 KB rows).
+long blocks_per_cu(long groups, bool norm, int epi, int wf, long k) {
+  if (wf == WF_BF16 && (epi == EPI_RESIDUAL ? !norm : (norm && epi == EPI_SWIGLU))) {
+    const long want = epi == EPI_RESIDUAL ? 2 : 3;
+    const long cus = device_cus();
+    for (long pc = 1; pc <= 8; pc *= 2)
+      if (groups == pc * 4 * cus * want) return pc;
+  }
+  if (norm) return wf == WF_BF16 ? 2 : (k > 1024 ? 4 : 8);
+  return 8;
+}
+
 template <int R, int S, int U, bool NORM, int EPI, int WF>
 int launch_vec(const GemvArgs& a, hipStream_t st) {
   const long groups = (a.n + R - 1) / R;
-  // RMSNorm kernels pay their prologue once per block: two longer-lived
-  // blocks per CU beat four (measured from 3072 to 151936 row groups: e.g. the
-  // 6144-row, K = 4096 QKV projection takes 9.9 us at two, 10.6 us at four).
-  // Kernels without a prologue fill the CU.
-  // 8-bit rows are half as long, so a wave holds half the bytes in flight:
-  // their norm kernels keep four blocks per CU (eight for 1 KB rows).
-  long per_cu = 8;
-  if (NORM && WF == WF_BF16) per_cu = 2;
-  if (NORM && WF != WF_BF16) per_cu = a.k > 1024 ? 4 : 8;
-  const long blocks = grid_for(groups, per_cu);
+  const long blocks = grid_for(groups, blocks_per_cu(groups, NORM, EPI, WF, a.k));
   const size_t lds = NORM ? static_cast<size_t>(a.k) * 2 : 0;
   hipLaunchKernelGGL((gemv_vec<R, S, U, NORM, EPI, WF>), dim3(blocks), dim3(kBlock), lds, st, a);
   if (EPI == EPI_ARGMAX) return finish_argmax(a, blocks, st);
@@ -521,14 +537,14 @@ int dispatch(GemvArgs& a, hipStream_t st) {
 bool gemv_plain_layout(long n, long k, int format, long* blocks, int* rows) {
   const int epv = format == WF_BF16 ? Fmt<WF_BF16>::kPerVec : Fmt<WF_INT8>::kPerVec;
   if (n <= 0 || k <= 0 || k > kMaxK || k % epv != 0) return false;
-  // Mirrors dispatch() for S = 1 and no prologue.
+  // Mirrors dispatch() for the residual epilogue (S = 1, no prologue).
   const int chunks = static_cast<int>((k / epv + 63) / 64);
   const bool many_rows = n >= 4 * kWavesPerCu * device_cus();
   int r = 1;
   if (format != WF_BF16 && chunks == 1) r = many_rows ? 4 : 1;
   else if (format != WF_BF16 && chunks > 8) r = 2;
   else if (chunks <= 2) r = many_rows ? 4 : 1;
-  *blocks = grid_for((n + r - 1) / r, 8);
+  *blocks = grid_for((n + r - 1) / r, blocks_per_cu((n + r - 1) / r, false, EPI_RESIDUAL, format, k));
   *rows = 4 * r;
   return true;
 }
