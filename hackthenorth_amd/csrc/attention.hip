@@ -1999,6 +1999,11 @@ struct NextWeights {
 // holds at least 32 KB of LDS, so they run on CUs the attention leaves free.
 constexpr int kPrefetchPerXcd = 8;
 constexpr long kPrefetchXcdBytes = 3L << 20;
+// Long contexts (six tiles per split): the attention outlasts the prefetch by
+// far and its 176 blocks crowd the CUs, so half as many prefetch blocks (8B
+// int8 / fp8 at context 8192: 2.223 -> 2.186 and 2.133 -> 2.096 ms per step;
+// two per XCD outlast the attention, 2.44 ms).
+constexpr int kPrefetchPerXcdLong = 4;
 
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
                   const NextWeights* next = nullptr) {
@@ -2099,7 +2104,7 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
     const long units = next->n / gemv_rows;  // whole spans only
     const long cap_units = 8 * kPrefetchXcdBytes / a.pf_unit_bytes;
     a.pf_units = units < cap_units ? units : cap_units;
-    a.pf_per_class = kPrefetchPerXcd;
+    a.pf_per_class = a.split >= 6 * kSplit ? kPrefetchPerXcdLong : kPrefetchPerXcd;
     const long pairs = static_cast<long>(a.B) * a.Hkv;
     a.attn_blocks = static_cast<int>(8 * ((pairs + 7) / 8) * a.splits);
   }
