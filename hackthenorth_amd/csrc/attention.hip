@@ -1789,6 +1789,258 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   if (a.done) merge_tail(a, b, kvh, &last_split);
 }
 
+// ------------------------------------------------------------------ causal prefill
+
+// Operand reads of the prefill kernel's staged tiles (LDS-direct data, read
+// by inline asm: the compiler would wait for every load in flight before an
+// ordinary LDS read of such a buffer).
+// K operand of one 32-dim step for the four 16-slot M-tiles of a 64-slot tile.
+__device__ __forceinline__ void read_k_pf(uint32_t addr, u32x4 (&k)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:0\n\t"
+      "ds_read_b128 %1, %4 offset:4096\n\t"
+      "ds_read_b128 %2, %4 offset:8192\n\t"
+      "ds_read_b128 %3, %4 offset:12288\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
+      : "v"(addr)
+      : "memory");
+}
+
+// V^T operands of one 16-slot M-tile (byte offset OFF in the V half): element
+// k of vt[j] is V[slot 4 * quad + k][dim 16 * j + col], at va[j] + OFF + 256 k.
+template <int OFF>
+__device__ __forceinline__ void read_vt_pf(const uint32_t (&va)[8], uint2 (&vt)[8]) {
+  uint32_t w[32];
+  asm volatile(
+      "ds_read_u16 %0, %32 offset:%40\n\t"
+      "ds_read_u16 %1, %32 offset:%41\n\t"
+      "ds_read_u16 %2, %32 offset:%42\n\t"
+      "ds_read_u16 %3, %32 offset:%43\n\t"
+      "ds_read_u16 %4, %33 offset:%40\n\t"
+      "ds_read_u16 %5, %33 offset:%41\n\t"
+      "ds_read_u16 %6, %33 offset:%42\n\t"
+      "ds_read_u16 %7, %33 offset:%43\n\t"
+      "ds_read_u16 %8, %34 offset:%40\n\t"
+      "ds_read_u16 %9, %34 offset:%41\n\t"
+      "ds_read_u16 %10, %34 offset:%42\n\t"
+      "ds_read_u16 %11, %34 offset:%43\n\t"
+      "ds_read_u16 %12, %35 offset:%40\n\t"
+      "ds_read_u16 %13, %35 offset:%41\n\t"
+      "ds_read_u16 %14, %35 offset:%42\n\t"
+      "ds_read_u16 %15, %35 offset:%43\n\t"
+      "ds_read_u16 %16, %36 offset:%40\n\t"
+      "ds_read_u16 %17, %36 offset:%41\n\t"
+      "ds_read_u16 %18, %36 offset:%42\n\t"
+      "ds_read_u16 %19, %36 offset:%43\n\t"
+      "ds_read_u16 %20, %37 offset:%40\n\t"
+      "ds_read_u16 %21, %37 offset:%41\n\t"
+      "ds_read_u16 %22, %37 offset:%42\n\t"
+      "ds_read_u16 %23, %37 offset:%43\n\t"
+      "ds_read_u16 %24, %38 offset:%40\n\t"
+      "ds_read_u16 %25, %38 offset:%41\n\t"
+      "ds_read_u16 %26, %38 offset:%42\n\t"
+      "ds_read_u16 %27, %38 offset:%43\n\t"
+      "ds_read_u16 %28, %39 offset:%40\n\t"
+      "ds_read_u16 %29, %39 offset:%41\n\t"
+      "ds_read_u16 %30, %39 offset:%42\n\t"
+      "ds_read_u16 %31, %39 offset:%43\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+        "=&v"(w[6]), "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]),
+        "=&v"(w[12]), "=&v"(w[13]), "=&v"(w[14]), "=&v"(w[15]), "=&v"(w[16]), "=&v"(w[17]),
+        "=&v"(w[18]), "=&v"(w[19]), "=&v"(w[20]), "=&v"(w[21]), "=&v"(w[22]), "=&v"(w[23]),
+        "=&v"(w[24]), "=&v"(w[25]), "=&v"(w[26]), "=&v"(w[27]), "=&v"(w[28]), "=&v"(w[29]),
+        "=&v"(w[30]), "=&v"(w[31])
+      : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]),
+        "v"(va[7]), "n"(OFF), "n"(OFF + 256), "n"(OFF + 512), "n"(OFF + 768)
+      : "memory");
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    vt[j] = make_uint2(w[4 * j] | (w[4 * j + 1] << 16), w[4 * j + 2] | (w[4 * j + 3] << 16));
+}
+
+constexpr int kPfQ = 64;                          // queries per prefill block
+constexpr int kPfTileBytes = 2 * kSplit * D * 2;  // K then V of one staged 64-slot tile
+
+// Causal attention over many queries per sequence (a prompt's prefill): one
+// launch per layer, no split, no merge. Block = (64-query tile, query head h,
+// batch b), four waves of 16 queries. The block stages each 64-slot K/V tile
+// of kv head h / G once for its four waves (each wave a quarter, LDS-direct,
+// the next tile in flight), then every wave multiplies all 64 slots against
+// its queries on the matrix cores as the decode kernel does per 16-slot
+// group: S^T = K Q^T (slots as M, queries as N: four 16-slot M-tiles x four
+// 32-dim steps), an online softmax per query in base 2, O^T += V^T P^T with P
+// as hi/lo bf16 halves (weights keep ~16 bits; the denominator sums the fp32
+// weights). A query sees slots <= its own position (masked per lane); the
+// block reads tiles up to its largest position, the latest query tiles
+// first. K rows are staged rotated (chunk c of slot s at column (c + s) % 16)
+// and V rows by two chunks per four slots, so both operand reads are free of
+// bank conflicts.
+__global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char ring[];  // two staged tiles
+  __shared__ int wave_pos[kBlock / kWave];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, quad = lane >> 4;
+  const int ntq = (a.Q + kPfQ - 1) / kPfQ;
+  const int qt = ntq - 1 - static_cast<int>(blockIdx.x);  // latest queries first
+  const int h = blockIdx.y, b = blockIdx.z, kvh = h / a.G;
+  const int t = qt * kPfQ + wave * 16 + col;  // this lane's query
+  const int tq = t < a.Q ? t : a.Q - 1;
+  // Visible slots [0, pos]; a position past the cache sees every slot, a
+  // negative one (and a padding query) none.
+  const int64_t pv = a.pos[tq];
+  const int pos = t >= a.Q || pv < 0 ? -1 : (pv >= a.cap ? static_cast<int>(a.cap) - 1 : static_cast<int>(pv));
+  // B operand of S^T = K Q^T: dims 32 ks + 8 quad .. + 7 of this lane's query.
+  const bf16_t* qrow = a.q + b * a.q_sb + h * a.q_sh + tq * a.q_st + 8 * quad;
+  u32x4 qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 32 * ks);
+  const float wmax = wave_max(static_cast<float>(pos));     // exact: |pos| < 2^24
+  const float wmin = -wave_max(-static_cast<float>(pos));
+  if (lane == 0) wave_pos[wave] = static_cast<int>(wmax);
+  lds_barrier();
+  int bmax = wave_pos[0];
+#pragma unroll
+  for (int w = 1; w < kBlock / kWave; ++w) bmax = wave_pos[w] > bmax ? wave_pos[w] : bmax;
+  const int nkt = bmax < 0 ? 0 : bmax / kSplit + 1;  // tiles [0, nkt) hold every visible slot
+  const int wave_last = static_cast<int>(wmax), wave_first = static_cast<int>(wmin);
+
+  // Staging: wave w loads slots 16 w .. 16 w + 15 of each tile (K, then V),
+  // through descriptors over the slots up to the block's largest position:
+  // later slots (the cache may hold anything there, NaN included) read as
+  // zeros, so masked weights never multiply NaN.
+  const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
+  const uint32_t range = static_cast<uint32_t>(bmax + 1) * D * 2;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base, range);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base, range);
+  uint32_t kvoff[4], vvoff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int sl = 4 * u + (lane >> 4);
+    kvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - sl) & 15) * 16);
+    vvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - 2 * u) & 15) * 16);
+  }
+  auto stage = [&](int kt) {
+    unsigned char* tb = ring + (kt & 1) * kPfTileBytes + wave * 4096;
+    const uint32_t off = static_cast<uint32_t>(kt * kSplit + wave * 16) * D * 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(tb + u * 1024), 16, kvoff[u], off, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(tb + kSplit * D * 2 + u * 1024), 16,
+                                               vvoff[u], off, 0, 0);
+  };
+  if (nkt > 0) stage(0);
+  if (nkt > 1) stage(1);
+
+  // Operand addresses in tile buffer 0 (buffer 1 is kPfTileBytes further):
+  // K slot 16 mt + col, chunk 4 ks + quad, rotated by the slot; V^T dim
+  // 16 j + col of slots 16 mt + 4 quad + k, rotated by 2 quad.
+  const uint32_t ring_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)ring));
+  uint32_t kaddr[4], vaddr[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    kaddr[ks] = ring_base + static_cast<uint32_t>(col * 256 + (((4 * ks + quad + col) & 15) * 16));
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    vaddr[j] = ring_base + kSplit * D * 2 +
+               static_cast<uint32_t>(quad * 1024 + (((2 * j + (col >> 3) + 2 * quad) & 15) * 16) +
+                                     (col & 7) * 2);
+
+  const float scale2 = a.scale * 1.4426950408889634f;  // log2(e) / sqrt(D)
+  f32x4_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  for (int kt = 0; kt < nkt; ++kt) {
+    // This wave's part of tile kt has landed (tile kt + 1 may still be in
+    // flight), then everyone's.
+    if (kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    const int s0 = kt * kSplit;
+    if (s0 <= wave_last) {  // wave-uniform: some slot of the tile is visible to the wave
+      const uint32_t tb = static_cast<uint32_t>((kt & 1) * kPfTileBytes);
+      f32x4_t st[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) st[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4 kf[4];
+        read_k_pf(kaddr[ks] + tb, kf);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mt]),
+                                                           __builtin_bit_cast(bf16x8_t, qf[ks]),
+                                                           st[mt], 0, 0, 0);
+      }
+      // Scores in base 2; slots past the query's position masked unless the
+      // whole tile is visible to every query of the wave.
+      const bool all_visible = s0 + kSplit - 1 <= wave_first;
+      float sc[4][4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = st[mt][i] * scale2;
+          if (!all_visible) v = s0 + 16 * mt + 4 * quad + i <= pos ? v : -INFINITY;
+          sc[mt][i] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      tmax = quad_max(tmax);
+      const float m_new = fmaxf(m, tmax);
+      // A query with nothing visible yet keeps weight 0 (no inf - inf).
+      const float ms = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while m is -inf
+      l *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+      m = m_new;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[mt][i] - ms);
+        l += (p[0] + p[1]) + (p[2] + p[3]);
+        const uint2 pb = make_uint2(pack_bf2(p[0], p[1]), pack_bf2(p[2], p[3]));
+        const uint2 pl = make_uint2(pack_bf2(p[0] - bf_lo(pb.x), p[1] - bf_hi(pb.x)),
+                                    pack_bf2(p[2] - bf_lo(pb.y), p[3] - bf_hi(pb.y)));
+        const uint4 phl = make_uint4(pb.x, pb.y, pl.x, pl.y);
+        uint32_t va[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) va[j] = vaddr[j] + tb;
+        uint2 vt[8];
+        if (mt == 0) read_vt_pf<0>(va, vt);
+        else if (mt == 1) read_vt_pf<4096>(va, vt);
+        else if (mt == 2) read_vt_pf<8192>(va, vt);
+        else read_vt_pf<12288>(va, vt);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, make_uint4(vt[j].x, vt[j].y, vt[j].x, vt[j].y)),
+              __builtin_bit_cast(bf16x8_t, phl), acc[j], 0, 0, 0);
+      }
+    }
+    // Every wave has read tile kt before its buffer takes tile kt + 2.
+    lds_barrier();
+    if (kt + 2 < nkt) stage(kt + 2);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // O[query][dim 16 j + 4 quad + i] = acc[j][i] / (the four quads' sums).
+  const float ln = quad_sum(l);
+  if (t < a.Q) {
+    bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + static_cast<long>(t) * a.o_st + 4 * quad;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<uint2*>(dst + 16 * j) =
+          make_uint2(pack_bf2(acc[j][0] / ln, acc[j][1] / ln), pack_bf2(acc[j][2] / ln, acc[j][3] / ln));
+  }
+}
+
 // Merge of the split partials, one block per output row (b, h, t):
 //   out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
 // Each wave folds every fourth split with an online max (one pass over the
@@ -2005,6 +2257,27 @@ constexpr long kPrefetchXcdBytes = 3L << 20;
 // two per XCD outlast the attention, 2.44 ms).
 constexpr int kPrefetchPerXcdLong = 4;
 
+// Many queries per sequence (a prefill): the causal kernel, one launch, no
+// scratch. Needs 16-byte query fragments and 8-byte output stores.
+int run_prefill_attention(AttnArgs& a, hipStream_t st) {
+  if (a.B <= 0 || a.cap <= 0 || a.Q > (1 << 30) || a.Hq > 65535 || a.B > 65535)
+    return HTN_EUNSUPPORTED;
+  if (a.cap > (1L << 31) / (D * 2) - 2 * kSplit) return HTN_EUNSUPPORTED;  // 32-bit byte offsets
+  if ((reinterpret_cast<uintptr_t>(a.q) & 15u) || ((a.q_sb | a.q_sh | a.q_st) & 7) ||
+      (reinterpret_cast<uintptr_t>(a.out) & 7u) || ((a.o_sb | a.o_sh | a.o_st) & 3))
+    return HTN_EUNSUPPORTED;
+  a.scale = 1.0f / sqrtf(static_cast<float>(D));
+  const size_t lds = 2 * static_cast<size_t>(kPfTileBytes);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&attention_prefill), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(lds));
+  (void)attr;  // a refused size surfaces as a launch error
+  const dim3 grid(static_cast<unsigned>((a.Q + kPfQ - 1) / kPfQ), static_cast<unsigned>(a.Hq),
+                  static_cast<unsigned>(a.B));
+  hipLaunchKernelGGL(attention_prefill, grid, dim3(kBlock), lds, st, a);
+  return launch_status();
+}
+
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
                   const NextWeights* next = nullptr) {
   const int rows = a.G * a.Q;
@@ -2124,6 +2397,7 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
 
 extern "C" int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap) {
   if (B <= 0 || Hq <= 0 || Q <= 0 || cap <= 0) return 0;
+  if (Q > kMaxQ) return kCounterBytes;  // the prefill kernel keeps no partials
   // The smallest split the plan picks is kMinSplit slots.
   const long splits = (cap + kMinSplit - 1) / kMinSplit;
   return kCounterBytes + static_cast<long>(B) * Hq * Q * splits * (D + 2) * 4;
@@ -2188,6 +2462,7 @@ extern "C" int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, 
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
   a.B = static_cast<int>(B); a.Hq = static_cast<int>(Hq); a.Hkv = static_cast<int>(Hkv);
   a.G = static_cast<int>(Hq / Hkv); a.Q = static_cast<int>(Q);
+  if (Q > kMaxQ) return run_prefill_attention(a, static_cast<hipStream_t>(stream));
   return run_attention(false, a, scratch, static_cast<hipStream_t>(stream));
 }
 

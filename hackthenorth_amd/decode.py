@@ -142,11 +142,16 @@ def _decode_one(model, token_ids, cache, position, rotary, out=None, advance=Non
 
 
 def _attention_chunks(q, keys, values, positions, groups):
-    """grouped_attention over the T queries in chunks the kernel takes at once
-    (at most 8 queries and 32 query rows per kv head), written token-major:
-    returns [B * T, Hq * 128] rows for the output projection, no transpose."""
+    """grouped_attention over the T queries, written token-major: returns
+    [B * T, Hq * 128] rows for the output projection, no transpose. More than
+    8 queries (a prefill) go to the causal kernel in one launch; up to 8 (a
+    verify pass) in chunks the split kernel takes at once (at most 8 queries
+    and 32 query rows per kv head)."""
     b, heads, t, dim = q.shape
     out = torch.empty((b, t, heads, dim), dtype=q.dtype, device=q.device)
+    if t > 8:
+        grouped_attention(q, keys, values, positions, out=out.transpose(1, 2))
+        return out.view(b * t, heads * dim)
     step = max(1, min(8, 32 // groups))
     for s in range(0, t, step):
         e = min(t, s + step)

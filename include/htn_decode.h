@@ -286,7 +286,8 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
                         const int64_t* positions, void* out_q, void* out_k, int64_t B,
                         int64_t T, int64_t Hq, int64_t Hkv, htn_stream_t stream);
 
-/* Bytes of scratch the attention entry points need for these sizes. The first
+/* Bytes of scratch the attention entry points need for these sizes (for Q > 8,
+ * the causal many-query kernel, only the counter region). The first
  * HTN_ATTENTION_COUNTER_BYTES hold arrival counters: zero them once when the
  * buffer is allocated; every call leaves them zero. Calls sharing a scratch
  * buffer must be ordered (one stream). */
@@ -314,6 +315,11 @@ int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t ca
  * 8, for more than 256 (batch, kv head) pairs, for the streaming long-context
  * kernel, or with the environment variable HTN_ATTENTION_MERGE_LAUNCH=1, a
  * second launch merges instead. One launch when the context fits one split.
+ * More than 8 queries per sequence (a prompt's prefill): one causal launch,
+ * no split and no scratch use; q must be 16-byte aligned with element strides
+ * that are multiples of 8, out 8-byte aligned with strides that are multiples
+ * of 4 (HTN_EUNSUPPORTED otherwise). It plays the part of the reference's
+ * causal flash attention over the prompt (attention.py:92-98).
  * Replaces grouped_attention(q, k, v, positions), kernels/attention.py:213. */
 int htn_grouped_attention(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                           const void* keys, const void* values, int64_t cap,

@@ -281,6 +281,34 @@ def test_grouped_attention_matches_oracle_and_ignores_unwritten_slots(batch, que
     assert bits_equal(again, actual.cpu())
 
 
+# Many queries per sequence (prefill): the causal kernel in one launch.
+PREFILL_CASES = [
+    (1, 32, 8, 9, 0, 64),       # one past the split kernel's eight queries
+    (1, 32, 8, 200, 0, 256),    # from slot 0, a partial query tile
+    (2, 16, 8, 130, 37, 300),   # batches, after a cached prefix, capacity off a tile boundary
+    (1, 8, 8, 64, 1000, 1100),  # group size 1, one query tile
+    (1, 40, 8, 100, 5, 128),    # group size 5
+    (1, 32, 8, 2048, 0, 2304),  # the 8B prefill: 2048 queries from slot 0
+]
+
+
+@pytest.mark.parametrize("batch,heads,kv_heads,queries,first,capacity", PREFILL_CASES)
+def test_prefill_attention_matches_oracle(batch, heads, kv_heads, queries, first, capacity):
+    # Queries at positions first .. first + queries - 1, each seeing the slots
+    # up to its own; slots past the last position hold NaN and must not leak.
+    q = nrm(40, (batch, queries, heads, 128)).transpose(1, 2)
+    k, v = nrm(41, (batch, kv_heads, capacity, 128)), nrm(42, (batch, kv_heads, capacity, 128))
+    positions = torch.arange(first, first + queries)
+    expected = Q.attention(q, k, v, positions)
+    kd, vd = cuda(k), cuda(v)
+    kd[:, :, first + queries:] = float("nan")
+    vd[:, :, first + queries:] = float("nan")
+    out = torch.empty((batch, queries, heads, 128), dtype=torch.bfloat16, device="cuda")
+    A.grouped_attention(cuda(q.transpose(1, 2).contiguous()).transpose(1, 2), kd, vd,
+                        cuda(positions), out=out.transpose(1, 2))
+    close(out.transpose(1, 2), expected)
+
+
 @pytest.mark.parametrize("heads,kv_heads,position,capacity",
                          [(8, 8, 16, 40), (16, 8, 17, 600), (16, 8, 599, 600), (24, 8, 300, 301),
                           (64, 8, 255, 1024), (16, 8, 1000, 1100)])
