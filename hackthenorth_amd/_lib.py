@@ -53,6 +53,7 @@ SIGNATURES = {
     "htn_gemm_rows_scratch_bytes": [_I64, _I64, _I64, _I, _I],
     "htn_gemm_rows": [_P, _I64, _P, _F, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P,
                       _P],
+    "htn_gemm_tiles": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P],
     "htn_gemm_rows_residual_norm": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F,
                                     _P, _P, _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],

@@ -1,0 +1,283 @@
+// Projections of many rows at once (a prompt's prefill): y = x W^T over M
+// rows as a tiled GEMM on the matrix cores, one launch per projection.
+//
+// The multi-row kernel of gemm_rows.hip streams each weight once for up to
+// 128 rows and re-reads the rows' fragments per 16-column strip; past a few
+// hundred rows the arithmetic, not the weight stream, is the work, and a
+// 2-D tiling that reuses both operands from LDS does it with far fewer
+// instructions per multiply:
+//
+//  * block = 256 threads (2 x 2 waves) on a 128-row x 128-column output tile;
+//    each 64-deep k step stages the x tile (128 rows x 128 bytes) and the
+//    weight tile (128 rows x 128 bytes) into LDS with LDS-direct loads
+//    (16 KB each; chunk c of row r at column c ^ (r & 7), so the fragment
+//    reads of eight consecutive lanes hit eight different column groups),
+//    two steps in flight;
+//  * each wave multiplies a 64 x 64 quarter: D^T = W X^T on
+//    v_mfma_f32_16x16x32_bf16 (weight rows as M, x rows as N), so a lane
+//    ends with four consecutive output columns of one row (8-byte stores);
+//  * SwiGLU tiles interleave gate and up rows (32 of each per wave), so a
+//    lane holds the gate and up dot products of the same outputs;
+//  * blocks are laid out XCD-major: the blocks of one weight tile share an
+//    XCD (block L runs on XCD L % 8), so its L2 serves the tile to all of them.
+//
+// Epilogues keep the batch-one GEMV's bf16 boundaries (store, + residual,
+// SwiGLU); fp32 accumulation over k in 64-wide steps.
+#include "common.h"
+
+namespace htn {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+
+constexpr int kTm = 128;                  // x rows per block
+constexpr int kTn = 128;                  // weight rows per block
+constexpr int kTk = 64;                   // k per staged step
+constexpr int kTileBytes = kTm * kTk * 2; // one operand tile (16 KB)
+constexpr int kStageBytes = 2 * kTileBytes;
+
+struct TileArgs {
+  const bf16_t* x; long x_rs;
+  const bf16_t* w;
+  const bf16_t* res; long res_rs;
+  bf16_t* y; long y_rs;
+  int M, N, K;        // N: output columns (gate columns for SwiGLU)
+  int mtiles, ntiles; // output tiles along M and N
+};
+
+// Eight 16-byte operand fragments in one asm block: LDS-direct data is read by
+// inline asm (the compiler would wait for every load in flight before an
+// ordinary LDS read of such a buffer).
+__device__ __forceinline__ void read_frag8(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                           uint32_t a4, uint32_t a5, uint32_t a6, uint32_t a7,
+                                           u32x4 (&f)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]),
+        "=&v"(f[6]), "=&v"(f[7])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(a4), "v"(a5), "v"(a6), "v"(a7)
+      : "memory");
+}
+
+__device__ __forceinline__ void lds_barrier_t() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];  // two stages of x and weight tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;  // this wave's 64-row, 64-column quarter
+  const int col = lane & 15, quad = lane >> 4;
+  // XCD-major layout: block L on XCD L % 8 takes weight tile
+  // nt = (L / 8 / mtiles) * 8 + L % 8 and row tile (L / 8) % mtiles.
+  const int L = blockIdx.x, j = L >> 3;
+  const int nt = (j / a.mtiles) * 8 + (L & 7), mt = j - (j / a.mtiles) * a.mtiles;
+  if (nt >= a.ntiles) return;
+  const int m0 = mt * kTm;
+  // Weight rows of the tile: rows n0 .. n0 + 127, or for SwiGLU 64 output
+  // columns c0 .. c0 + 63 as four 32-row groups gate, up, gate, up.
+  constexpr bool SW = EPI == HTN_EPI_SWIGLU;
+  const int n0 = SW ? nt * 64 : nt * kTn;
+
+  // Staging: wave w loads x rows 32 w .. 32 w + 31 and weight rows 32 w ..
+  // 32 w + 31 of the tile, eight rows (1 KB) per instruction; lane l takes
+  // row 8 u + l / 8 of the wave's 32 and writes position l % 8 of it,
+  // loading source chunk (l % 8) ^ (row & 7). Both operands go through one
+  // descriptor per wave whose range ends at the last real row, so rows past
+  // M or past the weight's end read as zeros. For SwiGLU, wave w's 32 weight
+  // rows are group w: gate, up, gate, up rows of columns n0 + 32 (w / 2) ...
+  const int lr = lane >> 3, lp = lane & 7;
+  const long mrows = a.M - m0 < kTm ? a.M - m0 : kTm;
+  const __amdgpu_buffer_rsrc_t xrs =
+      buffer_rsrc(a.x + static_cast<long>(m0) * a.x_rs,
+                  static_cast<uint32_t>(mrows * a.x_rs * 2));
+  long wbase, wrows;
+  if (SW) {
+    const int c0 = n0 + (wave >> 1) * 32;
+    wbase = static_cast<long>((wave & 1) ? a.N : 0) + c0;
+    wrows = a.N - c0 < 32 ? (a.N - c0 > 0 ? a.N - c0 : 0) : 32;
+  } else {
+    wbase = n0 + 32 * wave;
+    wrows = a.N - wbase < 32 ? (a.N - wbase > 0 ? a.N - wbase : 0) : 32;
+  }
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(a.w + (wrows > 0 ? wbase : 0) * a.K,
+                                                 static_cast<uint32_t>(wrows * a.K * 2));
+  uint32_t xoff[4], woff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = 8 * u + lr;      // row within the wave's 32
+    const int r = 32 * wave + c;   // tile row
+    const int chunk = lp ^ (r & 7);
+    xoff[u] = static_cast<uint32_t>(r) * static_cast<uint32_t>(a.x_rs) * 2u + chunk * 16;
+    woff[u] = static_cast<uint32_t>(c) * static_cast<uint32_t>(a.K) * 2u + chunk * 16;
+  }
+  auto stage = [&](int ks) {
+    unsigned char* st = lds + (ks & 1) * kStageBytes;
+    const uint32_t ko = static_cast<uint32_t>(ks) * kTk * 2u;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr_t*)(st + (32 * wave + 8 * u) * 128), 16,
+                                               xoff[u], ko, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr_t*)(st + kTileBytes + (32 * wave + 8 * u) * 128),
+                                               16, woff[u], ko, 0, 0);
+  };
+
+  // Fragment addresses in stage 0 (stage 1 is kStageBytes further): k chunk
+  // 4 h + quad of row 16 t + col, un-swizzled.
+  const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t*)lds));
+  uint32_t wa[2][4], xa[2][4];  // [k half][tile]
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rw = 64 * wn + 16 * t + col, rx = 64 * wm + 16 * t + col;
+      const int c = 4 * h + quad;
+      wa[h][t] = base + kTileBytes + static_cast<uint32_t>(rw * 128 + ((c ^ (rw & 7)) * 16));
+      xa[h][t] = base + static_cast<uint32_t>(rx * 128 + ((c ^ (rx & 7)) * 16));
+    }
+
+  f32x4_t acc[4][4];  // [weight tile][x tile]: D^T rows = weight rows, columns = x rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = a.K / kTk;
+  stage(0);
+  if (nk > 1) stage(1);
+  for (int ks = 0; ks < nk; ++ks) {
+    // This wave's part of step ks has landed (step ks + 1 may be in flight),
+    // then everyone's.
+    if (ks + 1 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier_t();
+    const uint32_t so = static_cast<uint32_t>((ks & 1) * kStageBytes);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 f[8];
+      read_frag8(wa[h][0] + so, wa[h][1] + so, wa[h][2] + so, wa[h][3] + so, xa[h][0] + so,
+                 xa[h][1] + so, xa[h][2] + so, xa[h][3] + so, f);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, f[i]), __builtin_bit_cast(bf16x8_t, f[4 + t]), acc[i][t],
+              0, 0, 0);
+    }
+    // Every wave has read step ks before its stage takes step ks + 2.
+    lds_barrier_t();
+    if (ks + 2 < nk) stage(ks + 2);
+  }
+
+  // Lane (col, quad) holds, per weight tile i and x tile t, the outputs of
+  // x row 64 wm + 16 t + col and weight rows 64 wn + 16 i + 4 quad + (0..3).
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int m = m0 + 64 * wm + 16 * t + col;
+    if (m >= a.M) continue;
+    if constexpr (SW) {
+      // Weight tiles 0, 1 are gate columns c .. c + 31 and 2, 3 the up
+      // columns of the same outputs (c = n0 + 32 wn).
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int n = n0 + 32 * wn + 16 * i + 4 * quad;
+        if (n >= a.N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = silu_bf(round_bf(acc[i][t][e])) * round_bf(acc[i + 2][t][e]);
+        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
+        if (n + 4 <= a.N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+        } else {
+          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 64 * wn + 16 * i + 4 * quad;
+        if (n >= a.N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = acc[i][t][e];
+          if (EPI == HTN_EPI_RESIDUAL)
+            o[e] = round_bf(o[e]) + (n + e < a.N ? bf2f(a.res[static_cast<long>(m) * a.res_rs + n + e]) : 0.f);
+        }
+        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
+        if (n + 4 <= a.N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+        } else {
+          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+int launch_tiles(TileArgs& a, hipStream_t st) {
+  const size_t lds = 2 * static_cast<size_t>(kStageBytes);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&gemm_tiles_kernel<EPI>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  (void)attr;  // a refused size surfaces as a launch error
+  const long blocks = static_cast<long>((a.ntiles + 7) / 8) * 8 * a.mtiles;
+  hipLaunchKernelGGL((gemm_tiles_kernel<EPI>), dim3(static_cast<unsigned>(blocks)), dim3(256), lds,
+                     st, a);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace htn
+
+using namespace htn;
+
+extern "C" int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, int64_t n,
+                              int64_t k, int64_t rows, int epilogue, const void* residual,
+                              int64_t res_stride, void* y, int64_t y_stride,
+                              htn_stream_t stream) {
+  if (!x || !w || !y || rows <= 0 || n <= 0 || k <= 0) return HTN_EINVAL;
+  if (epilogue != HTN_EPI_STORE && epilogue != HTN_EPI_RESIDUAL && epilogue != HTN_EPI_SWIGLU)
+    return HTN_EINVAL;
+  if (epilogue == HTN_EPI_RESIDUAL && (!residual || res_stride < n)) return HTN_EINVAL;
+  if (y_stride < n || x_stride < k) return HTN_EINVAL;  // rows must not overlap
+  // 64-wide k steps of 16-byte chunks; 8-byte output stores; 32-bit offsets.
+  if (k % kTk || k > (1L << 20) || x_stride % 8 || y_stride % 4 || !aligned16(x) || !aligned16(w) ||
+      (reinterpret_cast<uintptr_t>(y) & 7u))
+    return HTN_EUNSUPPORTED;
+  const long wrows = epilogue == HTN_EPI_SWIGLU ? 2 * n : n;
+  if (static_cast<long>(kTm) * x_stride * 2 >= (1L << 31) || k * 2 >= (1L << 31) ||
+      wrows >= (1L << 31) || rows >= (1L << 31))
+    return HTN_EUNSUPPORTED;
+  TileArgs a{};
+  a.x = static_cast<const bf16_t*>(x); a.x_rs = x_stride;
+  a.w = static_cast<const bf16_t*>(w);
+  a.res = static_cast<const bf16_t*>(residual); a.res_rs = res_stride;
+  a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
+  a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
+  a.mtiles = static_cast<int>((rows + kTm - 1) / kTm);
+  a.ntiles = static_cast<int>(epilogue == HTN_EPI_SWIGLU ? (n + 63) / 64 : (n + kTn - 1) / kTn);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (epilogue) {
+    case HTN_EPI_STORE: return launch_tiles<HTN_EPI_STORE>(a, st);
+    case HTN_EPI_RESIDUAL: return launch_tiles<HTN_EPI_RESIDUAL>(a, st);
+    default: return launch_tiles<HTN_EPI_SWIGLU>(a, st);
+  }
+}

@@ -5,13 +5,33 @@ runs its multi-row projections as Triton GEMM tiles (dryft/engine/
 projections.py:168-183, kernels/gateup.py:40-58, kernels/split_down.py:85-101).
 Here every multi-row projection is one htn_gemm_rows launch (plus a K-split
 reduction when the strips alone cannot fill the GPU) with the batch-one
-GEMVs' bf16 rounding boundaries. Larger row counts run in chunks of 128.
+GEMVs' bf16 rounding boundaries. From TILE_ROWS rows on (a prompt's
+prefill) the projections run as one tiled GEMM launch each (htn_gemm_tiles,
+both operands staged in LDS), an input RMSNorm as its own row-norm launch;
+otherwise rows run in chunks of 128.
 """
 import torch
 
 from .. import _lib
 
 MAX_ROWS = 128
+TILE_ROWS = 256
+
+
+def _tiles(x, weight, n, epilogue, residual=None, gain=None, eps=1e-6):
+    """One htn_gemm_tiles launch over every row of x (after the rows' RMSNorm
+    with `gain`, when given); returns the [M, n] output."""
+    rows, k = x.shape
+    if gain is not None:
+        xn = torch.empty((rows, k), dtype=x.dtype, device=x.device)
+        _lib.call("htn_rms_norm", _lib.ptr(x), x.stride(0), _lib.ptr(gain), _lib.ptr(xn), rows, k,
+                  float(eps), _lib.stream(x.device))
+        x = xn
+    out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    _lib.call("htn_gemm_tiles", _lib.ptr(x), x.stride(0), _lib.ptr(weight), n, k, rows, epilogue,
+              _lib.ptr(residual), residual.stride(0) if residual is not None else 0,
+              _lib.ptr(out), out.stride(0), _lib.stream(x.device))
+    return out
 
 
 def _scratch(device, rows, n, k, epilogue, norm):
@@ -47,6 +67,8 @@ def projection_rows(x, weight, gain=None, eps=1e-6):
     """bf16(W x_m) for every row m of x [M, K]; gain applies RMSNorm first."""
     _check(x, weight)
     _lib.require_gpu(x, weight, gain)
+    if x.shape[0] >= TILE_ROWS:
+        return _tiles(x, weight, weight.shape[0], _lib.EPI_STORE, gain=gain, eps=eps)
     out = torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
     for s, e in _chunks(x.shape[0]):
         _launch(x[s:e], weight, weight.shape[0], _lib.EPI_STORE, gain, eps, out=out[s:e])
@@ -60,6 +82,8 @@ def residual_rows(x, weight, residual):
             or residual.stride(1) != 1:
         raise ValueError("residual must be bf16 [M, N] with unit column stride")
     _lib.require_gpu(x, weight, residual)
+    if x.shape[0] >= TILE_ROWS:
+        return _tiles(x, weight, weight.shape[0], _lib.EPI_RESIDUAL, residual=residual)
     out = torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
     for s, e in _chunks(x.shape[0]):
         _launch(x[s:e], weight, weight.shape[0], _lib.EPI_RESIDUAL, residual=residual[s:e],
@@ -88,6 +112,12 @@ def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
             or not gain.is_contiguous():
         raise ValueError("gain must be a contiguous bf16 [N] vector")
     _lib.require_gpu(x, weight, residual, gain)
+    if x.shape[0] >= TILE_ROWS:
+        out = _tiles(x, weight, n, _lib.EPI_RESIDUAL, residual=residual)
+        normed = torch.empty_like(out)
+        _lib.call("htn_rms_norm", _lib.ptr(out), out.stride(0), _lib.ptr(gain), _lib.ptr(normed),
+                  out.shape[0], n, float(eps), _lib.stream(x.device))
+        return out, normed
     out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
     normed = torch.empty_like(out)
     for s, e in _chunks(x.shape[0]):
@@ -107,6 +137,8 @@ def swiglu_rows(x, gate_up_weight, gain=None, eps=1e-6):
         raise ValueError("packed gate/up width must be even")
     _lib.require_gpu(x, gate_up_weight, gain)
     n = gate_up_weight.shape[0] // 2
+    if x.shape[0] >= TILE_ROWS:
+        return _tiles(x, gate_up_weight, n, _lib.EPI_SWIGLU, gain=gain, eps=eps)
     out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
     for s, e in _chunks(x.shape[0]):
         _launch(x[s:e], gate_up_weight, n, _lib.EPI_SWIGLU, gain, eps, out=out[s:e])

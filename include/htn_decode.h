@@ -235,6 +235,23 @@ int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w, 
                                 int64_t res_stride, void* y, int64_t y_stride, const void* gain,
                                 float eps, void* normed, void* scratch, htn_stream_t stream);
 
+/* The projection of many rows at once (a prompt's prefill: hundreds to
+ * thousands of rows): y = x W^T as a tiled GEMM on the matrix cores, one
+ * launch, 128 x 128 output tiles, both operands staged in LDS (weight tiles
+ * reused from the L2 of one XCD by every row tile). Epilogues HTN_EPI_STORE,
+ * HTN_EPI_RESIDUAL and HTN_EPI_SWIGLU as htn_gemm_rows (w holds 2n rows for
+ * SwiGLU: gate rows, then up rows); no input RMSNorm (normalise the rows
+ * first with htn_rms_norm). Rows are x[m, :k] with row stride x_stride; y
+ * (and the residual) [rows, n] with row strides y_stride (res_stride). k must
+ * be a multiple of 64 and at most 2^20, x_stride a multiple of 8 and
+ * y_stride of 4, x and w 16-byte and y 8-byte aligned. fp32 accumulation
+ * over k in 64-wide steps; bf16 rounding boundaries as htn_gemm_rows.
+ * Replaces the reference's projections over the whole prompt in its prefill
+ * forward (prefill.py:6-26 -> DecodeState.prefill, decode.py:156-166). */
+int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, int64_t n, int64_t k,
+                   int64_t rows, int epilogue, const void* residual, int64_t res_stride, void* y,
+                   int64_t y_stride, htn_stream_t stream);
+
 /* SwiGLU of `rows` (1..32) activation rows x[m, :k] (row stride x_stride)
  * by the interleaved K-major weight w[k, 2 * width] (row-major, w[k, 2i] the
  * gate and w[k, 2i + 1] the up weight of output i):

@@ -57,6 +57,44 @@ def test_projection_rows_match_oracle(m, n, k):
                                Q.silu_mul(gu[:, :n], gu[:, n:]).float(), atol=2e-2, rtol=2e-2)
 
 
+# From RW.TILE_ROWS rows on (a prefill) the projections are one tiled GEMM
+# launch each: ragged row counts, widths off the 128 / 64-column tiles.
+TILE_CASES = [(256, 1024, 1024), (300, 2560, 2560), (1000, 1000, 4096), (513, 9728, 2560),
+              (2048, 4096, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", TILE_CASES)
+def test_tiled_projection_rows_match_oracle(m, n, k):
+    assert m >= RW.TILE_ROWS
+    w = nrm(40, (2 * n, k), std=0.02)
+    x, g, res = nrm(41, (m, k)), nrm(42, (k,)), nrm(43, (m, n))
+    wd, xd, gd, rd = w.cuda(), x.cuda(), g.cuda(), res.cuda()
+    top = wd[:n].contiguous()
+    within_one_ulp(RW.projection_rows(xd, top), Q.linear(x, w[:n]))
+    # With the input RMSNorm: the row-norm kernel's output can differ from the
+    # oracle's norm by one bf16 ulp in rare elements (its own bar); the GEMM
+    # is held to one output ulp on the rows it was given, and the whole to the
+    # oracle within the general bar.
+    normed = Q.rms_norm(x, g, 1e-6)
+    with_norm = RW.projection_rows(xd, top, gd, 1e-6)
+    within_one_ulp(with_norm, Q.linear(rms_norm(xd, gd, 1e-6).cpu(), w[:n]))
+    torch.testing.assert_close(with_norm.cpu().float(), Q.linear(normed, w[:n]).float(),
+                               atol=2e-2, rtol=2e-2)
+    expected = Q.output_residual(x, w[:n], res)
+    torch.testing.assert_close(RW.residual_rows(xd, top, rd).cpu().float(), expected.float(),
+                               atol=2e-2, rtol=2e-2)
+    gn = nrm(44, (n,)).cuda()
+    out, nxt = RW.residual_norm_rows(xd, top, rd, gn, 1e-6)
+    torch.testing.assert_close(out.cpu().float(), expected.float(), atol=2e-2, rtol=2e-2)
+    if n <= 8192:   # the standalone norm kernel takes rows of up to 8192 columns
+        assert torch.equal(nxt.cpu(), rms_norm(out, gn, 1e-6).cpu())
+    torch.testing.assert_close(nxt.cpu().float(), Q.rms_norm(out.cpu(), gn.cpu(), 1e-6).float(),
+                               atol=2e-2, rtol=2e-2)
+    gu = Q.linear(normed, w)
+    torch.testing.assert_close(RW.swiglu_rows(xd, wd, gd, 1e-6).cpu().float(),
+                               Q.silu_mul(gu[:, :n], gu[:, n:]).float(), atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("m", [1, 3, 8, 32])
 def test_rows_match_the_batch_one_gemvs(m):
     n, k = 1024, 3072
