@@ -1912,9 +1912,9 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
   // later slots (the cache may hold anything there, NaN included) read as
   // zeros, so masked weights never multiply NaN.
   const long kv_base = (static_cast<long>(b) * a.Hkv + kvh) * a.cap * D;
-  const uint32_t range = static_cast<uint32_t>(bmax + 1) * D * 2;
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.keys + kv_base, range);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.values + kv_base, range);
+  const uint32_t range = static_cast<uint32_t>(bmax + 1) * D * 2;  // block-uniform (from LDS)
+  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(a.keys + kv_base, range);
+  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(a.values + kv_base, range);
   uint32_t kvoff[4], vvoff[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {

@@ -121,6 +121,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                            static_cast<int>(bytes), 0x00020000);
 }
 
+// The same descriptor from a base and range that are uniform but that the
+// compiler cannot prove so (values selected per wave): readfirstlane keeps
+// them in scalar registers; a descriptor in vector registers makes every load
+// through it a per-lane descriptor loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+  return buffer_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo),
+                     __builtin_amdgcn_readfirstlane(bytes));
+}
+
 __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
                                                uint32_t soff) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);

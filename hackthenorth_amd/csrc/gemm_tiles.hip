@@ -12,7 +12,8 @@
 //    weight tile (128 rows x 128 bytes) into LDS with LDS-direct loads
 //    (16 KB each; chunk c of row r at column c ^ (r & 7), so the fragment
 //    reads of eight consecutive lanes hit eight different column groups),
-//    two steps in flight;
+//    the next step's loads in flight during this step's multiplies, one
+//    barrier per step;
 //  * each wave multiplies a 64 x 64 quarter: D^T = W X^T on
 //    v_mfma_f32_16x16x32_bf16 (weight rows as M, x rows as N), so a lane
 //    ends with four consecutive output columns of one row (8-byte stores);
@@ -49,10 +50,12 @@ struct TileArgs {
 
 // Eight 16-byte operand fragments in one asm block: LDS-direct data is read by
 // inline asm (the compiler would wait for every load in flight before an
-// ordinary LDS read of such a buffer).
-__device__ __forceinline__ void read_frag8(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
-                                           uint32_t a4, uint32_t a5, uint32_t a6, uint32_t a7,
-                                           u32x4 (&f)[8]) {
+// ordinary LDS read of such a buffer). The reads of the next k half are issued
+// before the multiplies of this one; the wait names the fragments as
+// operands, so no use of them moves above it.
+__device__ __forceinline__ void issue_frag8(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                            uint32_t a4, uint32_t a5, uint32_t a6, uint32_t a7,
+                                            u32x4 (&f)[8]) {
   asm volatile(
       "ds_read_b128 %0, %8\n\t"
       "ds_read_b128 %1, %9\n\t"
@@ -61,16 +64,87 @@ __device__ __forceinline__ void read_frag8(uint32_t a0, uint32_t a1, uint32_t a2
       "ds_read_b128 %4, %12\n\t"
       "ds_read_b128 %5, %13\n\t"
       "ds_read_b128 %6, %14\n\t"
-      "ds_read_b128 %7, %15\n\t"
-      "s_waitcnt lgkmcnt(0)"
+      "ds_read_b128 %7, %15"
       : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]),
         "=&v"(f[6]), "=&v"(f[7])
       : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(a4), "v"(a5), "v"(a6), "v"(a7)
       : "memory");
 }
 
+__device__ __forceinline__ void wait_frag8(u32x4 (&f)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                 "+v"(f[6]), "+v"(f[7])
+               :
+               : "memory");
+}
+
+// 16 multiplies of one k half: weight fragments f[0..3] x x fragments f[4..7].
+__device__ __forceinline__ void mfma_half(const u32x4 (&f)[8], f32x4_t (&acc)[4][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, f[i]), __builtin_bit_cast(bf16x8_t, f[4 + t]), acc[i][t], 0,
+          0, 0);
+}
+
 __device__ __forceinline__ void lds_barrier_t() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Epilogue of one wave's 64 x 64 quarter. Lane (col, quad) holds, per weight
+// tile i and x tile t, the outputs of x row mb + 16 t + col and weight rows
+// (output columns) nb + 16 i + 4 quad + (0..3); for SwiGLU tiles 0, 1 are the
+// gate and 2, 3 the up rows of output columns nb .. nb + 31.
+template <int EPI>
+__device__ __forceinline__ void store_tile(const TileArgs& a, const f32x4_t (&acc)[4][4], int mb,
+                                           int nb, int col, int quad) {
+  constexpr bool SW = EPI == HTN_EPI_SWIGLU;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int m = mb + 16 * t + col;
+    if (m >= a.M) continue;
+    if constexpr (SW) {
+      // Weight tiles 0, 1 are gate columns nb .. nb + 31 and 2, 3 the up
+      // columns of the same outputs.
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int n = nb + 16 * i + 4 * quad;
+        if (n >= a.N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = silu_bf(round_bf(acc[i][t][e])) * round_bf(acc[i + 2][t][e]);
+        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
+        if (n + 4 <= a.N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+        } else {
+          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = nb + 16 * i + 4 * quad;
+        if (n >= a.N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = acc[i][t][e];
+          if (EPI == HTN_EPI_RESIDUAL)
+            o[e] = round_bf(o[e]) + (n + e < a.N ? bf2f(a.res[static_cast<long>(m) * a.res_rs + n + e]) : 0.f);
+        }
+        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
+        if (n + 4 <= a.N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+        } else {
+          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
+        }
+      }
+    }
+  }
 }
 
 template <int EPI>
@@ -112,8 +186,8 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
     wbase = n0 + 32 * wave;
     wrows = a.N - wbase < 32 ? (a.N - wbase > 0 ? a.N - wbase : 0) : 32;
   }
-  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(a.w + (wrows > 0 ? wbase : 0) * a.K,
-                                                 static_cast<uint32_t>(wrows * a.K * 2));
+  const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(a.w + (wrows > 0 ? wbase : 0) * a.K,
+                                                  static_cast<uint32_t>(wrows * a.K * 2));
   uint32_t xoff[4], woff[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -158,77 +232,28 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
 
   const int nk = a.K / kTk;
   stage(0);
-  if (nk > 1) stage(1);
   for (int ks = 0; ks < nk; ++ks) {
-    // This wave's part of step ks has landed (step ks + 1 may be in flight),
-    // then everyone's.
-    if (ks + 1 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // This wave's part of step ks has landed; after the barrier everyone's
+    // has, and every wave has finished step ks - 1, whose stage step ks + 1
+    // now takes (in flight during this step's multiplies).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier_t();
+    if (ks + 1 < nk) stage(ks + 1);
     const uint32_t so = static_cast<uint32_t>((ks & 1) * kStageBytes);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 f[8];
-      read_frag8(wa[h][0] + so, wa[h][1] + so, wa[h][2] + so, wa[h][3] + so, xa[h][0] + so,
-                 xa[h][1] + so, xa[h][2] + so, xa[h][3] + so, f);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, f[i]), __builtin_bit_cast(bf16x8_t, f[4 + t]), acc[i][t],
-              0, 0, 0);
-    }
-    // Every wave has read step ks before its stage takes step ks + 2.
-    lds_barrier_t();
-    if (ks + 2 < nk) stage(ks + 2);
+    u32x4 f0[8], f1[8];
+    issue_frag8(wa[0][0] + so, wa[0][1] + so, wa[0][2] + so, wa[0][3] + so, xa[0][0] + so,
+                xa[0][1] + so, xa[0][2] + so, xa[0][3] + so, f0);
+    wait_frag8(f0);
+    issue_frag8(wa[1][0] + so, wa[1][1] + so, wa[1][2] + so, wa[1][3] + so, xa[1][0] + so,
+                xa[1][1] + so, xa[1][2] + so, xa[1][3] + so, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_half(f0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_frag8(f1);
+    mfma_half(f1, acc);
   }
 
-  // Lane (col, quad) holds, per weight tile i and x tile t, the outputs of
-  // x row 64 wm + 16 t + col and weight rows 64 wn + 16 i + 4 quad + (0..3).
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int m = m0 + 64 * wm + 16 * t + col;
-    if (m >= a.M) continue;
-    if constexpr (SW) {
-      // Weight tiles 0, 1 are gate columns c .. c + 31 and 2, 3 the up
-      // columns of the same outputs (c = n0 + 32 wn).
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int n = n0 + 32 * wn + 16 * i + 4 * quad;
-        if (n >= a.N) continue;
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = silu_bf(round_bf(acc[i][t][e])) * round_bf(acc[i + 2][t][e]);
-        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
-        if (n + 4 <= a.N) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
-        } else {
-          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int n = n0 + 64 * wn + 16 * i + 4 * quad;
-        if (n >= a.N) continue;
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[e] = acc[i][t][e];
-          if (EPI == HTN_EPI_RESIDUAL)
-            o[e] = round_bf(o[e]) + (n + e < a.N ? bf2f(a.res[static_cast<long>(m) * a.res_rs + n + e]) : 0.f);
-        }
-        bf16_t* dst = a.y + static_cast<long>(m) * a.y_rs + n;
-        if (n + 4 <= a.N) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
-        } else {
-          for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
-        }
-      }
-    }
-  }
+  store_tile<EPI>(a, acc, m0 + 64 * wm, SW ? n0 + 32 * wn : n0 + 64 * wn, col, quad);
 }
 
 template <int EPI>
@@ -273,8 +298,8 @@ extern "C" int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, in
   a.y = static_cast<bf16_t*>(y); a.y_rs = y_stride;
   a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
   a.mtiles = static_cast<int>((rows + kTm - 1) / kTm);
-  a.ntiles = static_cast<int>(epilogue == HTN_EPI_SWIGLU ? (n + 63) / 64 : (n + kTn - 1) / kTn);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  a.ntiles = static_cast<int>(epilogue == HTN_EPI_SWIGLU ? (n + 63) / 64 : (n + kTn - 1) / kTn);
   switch (epilogue) {
     case HTN_EPI_STORE: return launch_tiles<HTN_EPI_STORE>(a, st);
     case HTN_EPI_RESIDUAL: return launch_tiles<HTN_EPI_RESIDUAL>(a, st);
