@@ -21,6 +21,12 @@ Also on the same line:
                   also the fraction of a device copy's measured bandwidth;
   decode_roofline bytes per generated token (every weight once + KV) x tok/s
                   against 8 TB/s;
+  prefill_s, prefill_kernels
+                  the captured batched prefill of the 2048-token prompt (replay
+                  time) and its matrix-core kernels at 2048 rows (the four tiled
+                  projection GEMMs and the causal attention, each over 8 layers
+                  back to back in a graph): microseconds, TFLOP/s and the
+                  fraction of the 2.5 PFLOP/s dense bf16 peak;
   cpu_baseline    the CPU oracle (torch eager, this host's cores) on a bounded
                   sample of the same workload: one batched prefill of the 2048-token
                   prompt, then 8 decode steps fed the GPU's tokens, reported as
@@ -324,6 +330,59 @@ def attention_kernel(model, ctx, rounds=4):
                 context=ctx, launches=len(calls))
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+
+
+def prefill_kernels(model, rows=2048, layers=8):
+    """The batched prefill's matrix-core kernels at `rows` prompt tokens: each
+    projection as the tiled GEMM launch the prefill makes (QKV store, O and
+    down + residual, gate/up + SwiGLU) and the causal attention, launched over
+    `layers` layers' weights back to back in a graph, timed with HIP events.
+    Work per launch: 2 M N K flops (N: weight rows, gate and up both counted),
+    causal attention 4 Hq D T (T + 1) / 2."""
+    from hackthenorth_amd.kernels import rows as RW
+    from hackthenorth_amd.kernels.attention import grouped_attention
+    c = model.config
+    dev = model.device
+    h = c.hidden_size
+    x = DR.normal_(torch.empty((rows, h), dtype=torch.bfloat16, device=dev), 5, 90, 1.0)
+    res = DR.normal_(torch.empty((rows, h), dtype=torch.bfloat16, device=dev), 5, 91, 1.0)
+    q_width = c.num_attention_heads * c.head_dim
+    inter = c.intermediate_size
+    a = DR.normal_(torch.empty((rows, q_width), dtype=torch.bfloat16, device=dev), 5, 92, 1.0)
+    m = DR.normal_(torch.empty((rows, inter), dtype=torch.bfloat16, device=dev), 5, 93, 1.0)
+    ls = model.layers[:layers]
+    out = {}
+    for name, fn, n, k in (
+            ("qkv", lambda l: RW.projection_rows(x, l.qkv_weight), sum(c.widths), h),
+            ("o_residual", lambda l: RW.residual_rows(a, l.o_weight, res), h, q_width),
+            ("gate_up_swiglu", lambda l: RW.swiglu_rows(x, l.gate_up_weight), 2 * inter, h),
+            ("down_residual", lambda l: RW.residual_rows(m, l.down_weight, res), h, inter)):
+        us = graph_launch_us([lambda l=l: fn(l) for l in ls], dev)
+        tflops = 2.0 * rows * n * k / us / 1e6
+        out[name] = {"us": round(us, 2), "tflops": round(tflops, 1),
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "n": n, "k": k}
+    cache = D.KVCache(model, 1, rows)
+    DR.normal_(cache.storage.view(-1), 21, 94, 1.0)
+    q = DR.normal_(torch.empty((1, c.num_attention_heads, rows, c.head_dim), dtype=torch.bfloat16,
+                               device=dev), 5, 95, 1.0)
+    pos = torch.arange(rows, device=dev)
+    o = torch.empty((1, rows, c.num_attention_heads, c.head_dim), dtype=torch.bfloat16, device=dev)
+    us = graph_launch_us([lambda i=i: grouped_attention(q, cache.keys[i], cache.values[i], pos,
+                                                        out=o.transpose(1, 2))
+                          for i in range(layers)], dev)
+    tflops = 4.0 * c.num_attention_heads * c.head_dim * rows * (rows + 1) / 2 / us / 1e6
+    out["attention_prefill"] = {"us": round(us, 2), "tflops": round(tflops, 1),
+                                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    del cache, x, res, a, m, q, o
+    return {"rows": rows, "peak_tflops": MFMA_BF16_PEAK_TFLOPS, **out}
+
+
+def prefill_kernels_no_grad(model, rows=2048):
+    with torch.inference_mode():
+        return prefill_kernels(model, rows)
+
+
 def copy_peak(nbytes=2 << 30, reps=5):
     """Device-to-device copy bandwidth (bytes read + written per second, GB/s)."""
     src = DR.normal_(torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda"), 9, 9, 1.0)
@@ -567,7 +626,7 @@ def main():
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
                     choices=("all", "qwen3-0.6b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
-                             "batched", "per-op"),
+                             "batched", "per-op", "prefill"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -595,6 +654,10 @@ def main():
             out = run_batched("qwen3-8b", 512, 32, (1, 4, 16), log)
         elif args.section == "per-op":
             out = {"per_op": per_op_microbench()}
+        elif args.section == "prefill":
+            model = Qwen3Model.random(shape_config("qwen3-8b"))
+            with torch.inference_mode():
+                out = {"prefill_kernels": prefill_kernels(model, args.prompt)}
         else:
             fmt = "int8" if args.section.endswith("int8") else "fp8_e4m3"
             r = run_decode("qwen3-8b", 8192, 128, args.warmup, log, weight_format=fmt,
@@ -649,6 +712,8 @@ def main():
                                 res["bytes_per_token"] * res["tok_s"] / 1e9 / read_gbs, 4),
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / res["bytes_per_token"], 1)},
         "prefill_s": round(res["prefill_s"], 3),
+        "prefill_tok_s": round(args.prompt / res["prefill_s"], 1),
+        "prefill_kernels": prefill_kernels_no_grad(res["model"], args.prompt),
         "first_tokens": [res["first"]] + res["tokens"][:15],
     }
     if not args.no_cpu_baseline and not args.headline_only:
