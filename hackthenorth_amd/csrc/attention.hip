@@ -1375,11 +1375,43 @@ __device__ __forceinline__ float quad_sum(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// K (rotated rows, per-lane source offsets kvoff) then V (plain rows) of this
-// wave's 16 slots of one tile: eight 1 KB LDS-direct loads, as stage_tile.
+// V^T operands by transpose reads (gfx950 ds_read_b64_tr_b16). Within each
+// 16-lane group the read returns to lane j element j % 4 of the 8 bytes at
+// the address of lane 4 k + j / 4, for k = 0..3 (the layout a probe of the
+// instruction showed). Lane (col, quad) of the P.V operand needs
+// V[slot 4 quad + k][dim 16 j + col], k = 0..3; so lane i of group quad
+// addresses slot 4 quad + i / 4, dims 16 j + 4 (i % 4) .. + 3, and one read
+// per j returns the four elements in order.
+template <int OFF>
+__device__ __forceinline__ void read_vt_tr(const uint32_t (&va)[8], uint2 (&vt)[8]) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 w[8];
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %1, %9 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %2, %10 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %3, %11 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %4, %12 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %5, %13 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %6, %14 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %7, %15 offset:%16\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+        "=&v"(w[6]), "=&v"(w[7])
+      : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]),
+        "v"(va[7]), "n"(OFF)
+      : "memory");
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vt[j] = make_uint2(w[j].x, w[j].y);
+}
+
+// K then V of this wave's 16 slots of one tile, both rows rotated through
+// per-lane source offsets (K: kvoff, chunk c of slot s at column (c + s) % 16;
+// V: vvoff, at column (c + 2 (s % 8)) % 16): eight 1 KB LDS-direct loads, as
+// stage_tile.
 __device__ __forceinline__ void stage_tile_mf(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
-                                              unsigned char* wave_lds, int lane,
-                                              const uint32_t (&kvoff)[4], uint32_t tile_off) {
+                                              unsigned char* wave_lds, const uint32_t (&kvoff)[4],
+                                              const uint32_t (&vvoff)[4], uint32_t tile_off) {
 #pragma unroll
   for (int u = 0; u < 4; ++u)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void_t*)(wave_lds + u * 1024), 16, kvoff[u],
@@ -1387,15 +1419,16 @@ __device__ __forceinline__ void stage_tile_mf(__amdgpu_buffer_rsrc_t krs, __amdg
 #pragma unroll
   for (int u = 0; u < 4; ++u)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void_t*)(wave_lds + 4096 + u * 1024), 16,
-                                             lane * 16, tile_off + u * 1024, 0, 0);
+                                             vvoff[u], tile_off, 0, 0);
 }
 
 // Wait until at most WAIT vector-memory operations are outstanding, then read
-// this lane's score operand (four 16-byte K chunks) and its V^T operands:
-// element k of vt[j] is V[slot 4 * quad + k][dim 16 * j + col].
+// this lane's score operand (four 16-byte K chunks) and its V^T operands by
+// transpose reads (read_vt_tr): element k of vt[j] is
+// V[slot 4 * quad + k][dim 16 * j + col].
 template <int WAIT>
-__device__ __forceinline__ void read_tile_mf(const uint32_t (&kaddr)[4], uint32_t vaddr, uint32_t ro,
-                                             uint4 (&k)[4], uint2 (&vt)[8]) {
+__device__ __forceinline__ void read_tile_mf(const uint32_t (&kaddr)[4], const uint32_t (&vaddr)[8],
+                                             uint32_t ro, uint4 (&k)[4], uint2 (&vt)[8]) {
   u32x4 k0, k1, k2, k3;
   asm volatile(
       "s_waitcnt vmcnt(%4)\n\t"
@@ -1406,60 +1439,14 @@ __device__ __forceinline__ void read_tile_mf(const uint32_t (&kaddr)[4], uint32_
       : "=&v"(k0), "=&v"(k1), "=&v"(k2), "=&v"(k3)
       : "n"(WAIT), "v"(kaddr[0] + ro), "v"(kaddr[1] + ro), "v"(kaddr[2] + ro), "v"(kaddr[3] + ro)
       : "memory");
-  // Each 16-bit element in its own register (zero-extended), packed after
-  // the reads: no instruction merges into a register another read still
-  // has in flight.
-  uint32_t w[32];
-  const uint32_t va = vaddr + ro;
-  asm volatile(
-      "ds_read_u16 %0, %32 offset:0\n\t"
-      "ds_read_u16 %1, %32 offset:256\n\t"
-      "ds_read_u16 %2, %32 offset:512\n\t"
-      "ds_read_u16 %3, %32 offset:768\n\t"
-      "ds_read_u16 %4, %32 offset:32\n\t"
-      "ds_read_u16 %5, %32 offset:288\n\t"
-      "ds_read_u16 %6, %32 offset:544\n\t"
-      "ds_read_u16 %7, %32 offset:800\n\t"
-      "ds_read_u16 %8, %32 offset:64\n\t"
-      "ds_read_u16 %9, %32 offset:320\n\t"
-      "ds_read_u16 %10, %32 offset:576\n\t"
-      "ds_read_u16 %11, %32 offset:832\n\t"
-      "ds_read_u16 %12, %32 offset:96\n\t"
-      "ds_read_u16 %13, %32 offset:352\n\t"
-      "ds_read_u16 %14, %32 offset:608\n\t"
-      "ds_read_u16 %15, %32 offset:864\n\t"
-      "ds_read_u16 %16, %32 offset:128\n\t"
-      "ds_read_u16 %17, %32 offset:384\n\t"
-      "ds_read_u16 %18, %32 offset:640\n\t"
-      "ds_read_u16 %19, %32 offset:896\n\t"
-      "ds_read_u16 %20, %32 offset:160\n\t"
-      "ds_read_u16 %21, %32 offset:416\n\t"
-      "ds_read_u16 %22, %32 offset:672\n\t"
-      "ds_read_u16 %23, %32 offset:928\n\t"
-      "ds_read_u16 %24, %32 offset:192\n\t"
-      "ds_read_u16 %25, %32 offset:448\n\t"
-      "ds_read_u16 %26, %32 offset:704\n\t"
-      "ds_read_u16 %27, %32 offset:960\n\t"
-      "ds_read_u16 %28, %32 offset:224\n\t"
-      "ds_read_u16 %29, %32 offset:480\n\t"
-      "ds_read_u16 %30, %32 offset:736\n\t"
-      "ds_read_u16 %31, %32 offset:992\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
-        "=&v"(w[6]), "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]),
-        "=&v"(w[12]), "=&v"(w[13]), "=&v"(w[14]), "=&v"(w[15]), "=&v"(w[16]), "=&v"(w[17]),
-        "=&v"(w[18]), "=&v"(w[19]), "=&v"(w[20]), "=&v"(w[21]), "=&v"(w[22]), "=&v"(w[23]),
-        "=&v"(w[24]), "=&v"(w[25]), "=&v"(w[26]), "=&v"(w[27]), "=&v"(w[28]), "=&v"(w[29]),
-        "=&v"(w[30]), "=&v"(w[31])
-      : "v"(va)
-      : "memory");
+  uint32_t va[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) va[j] = vaddr[j] + ro;
+  read_vt_tr<0>(va, vt);
   k[0] = make_uint4(k0.x, k0.y, k0.z, k0.w);
   k[1] = make_uint4(k1.x, k1.y, k1.z, k1.w);
   k[2] = make_uint4(k2.x, k2.y, k2.z, k2.w);
   k[3] = make_uint4(k3.x, k3.y, k3.z, k3.w);
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    vt[j] = make_uint2(w[4 * j] | (w[4 * j + 1] << 16), w[4 * j + 2] | (w[4 * j + 3] << 16));
 }
 
 template <int ROWS, int PRO, int RING>
@@ -1546,18 +1533,19 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   // K rows are staged rotated: chunk c of slot s sits at column (c + s) % 16
   // of the slot's 256-byte row, so the score operand's 16 slots (one column
   // each) fall in 16 different bank groups.
-  uint32_t kvoff[4];
+  uint32_t kvoff[4], vvoff[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int sl = 4 * u + (lane >> 4);
     kvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - sl) & 15) * 16);
+    vvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - 2 * (sl & 7)) & 15) * 16);
   }
   {
     const __amdgpu_buffer_rsrc_t krs0 = buffer_rsrc(kb, cap_range);
     const __amdgpu_buffer_rsrc_t vrs0 = buffer_rsrc(vb0, cap_range);
 #pragma unroll
     for (int t = 0; t < RING; ++t)
-      stage_tile_mf(krs0, vrs0, wave_ring + t * kLdsTile, lane, kvoff,
+      stage_tile_mf(krs0, vrs0, wave_ring + t * kLdsTile, kvoff, vvoff,
                     t * kSplit * D * 2 + wave_off);
   }
   // Positions outside [0, cap) never match a slot (clamped to -1 / cap).
@@ -1661,7 +1649,15 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     kaddr[j] = wave_base + static_cast<uint32_t>(col * 256 + ((4 * quad + j + col) & 15) * 16);
-  const uint32_t vaddr = wave_base + 4096 + static_cast<uint32_t>(quad * 1024 + col * 2);
+  // V^T transpose reads: slot r = 4 quad + col / 4, dims 16 j + 4 (col % 4)
+  // .. + 3, 8 bytes of chunk 2 j + (col % 4) / 2 at its rotated column.
+  uint32_t vaddr[8];
+  const int vr = 4 * quad + (col >> 2);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    vaddr[j] = wave_base + 4096 +
+               static_cast<uint32_t>(vr * 256 + (((2 * j + ((col & 3) >> 1) + 2 * (vr & 7)) & 15) * 16) +
+                                     (col & 1) * 8);
 
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
@@ -1758,7 +1754,7 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
     }
     const int tn = t + RING;
     if (tn < nt)  // wave-uniform
-      stage_tile_mf(krs, vrs, wave_ring + q * kLdsTile, lane, kvoff,
+      stage_tile_mf(krs, vrs, wave_ring + q * kLdsTile, kvoff, vvoff,
                     tn * kSplit * D * 2 + wave_off);
   }
   // Every staging load has landed before the block's LDS is released.
@@ -1807,59 +1803,6 @@ __device__ __forceinline__ void read_k_pf(uint32_t addr, u32x4 (&k)[4]) {
       : "memory");
 }
 
-// V^T operands of one 16-slot M-tile (byte offset OFF in the V half): element
-// k of vt[j] is V[slot 4 * quad + k][dim 16 * j + col], at va[j] + OFF + 256 k.
-template <int OFF>
-__device__ __forceinline__ void read_vt_pf(const uint32_t (&va)[8], uint2 (&vt)[8]) {
-  uint32_t w[32];
-  asm volatile(
-      "ds_read_u16 %0, %32 offset:%40\n\t"
-      "ds_read_u16 %1, %32 offset:%41\n\t"
-      "ds_read_u16 %2, %32 offset:%42\n\t"
-      "ds_read_u16 %3, %32 offset:%43\n\t"
-      "ds_read_u16 %4, %33 offset:%40\n\t"
-      "ds_read_u16 %5, %33 offset:%41\n\t"
-      "ds_read_u16 %6, %33 offset:%42\n\t"
-      "ds_read_u16 %7, %33 offset:%43\n\t"
-      "ds_read_u16 %8, %34 offset:%40\n\t"
-      "ds_read_u16 %9, %34 offset:%41\n\t"
-      "ds_read_u16 %10, %34 offset:%42\n\t"
-      "ds_read_u16 %11, %34 offset:%43\n\t"
-      "ds_read_u16 %12, %35 offset:%40\n\t"
-      "ds_read_u16 %13, %35 offset:%41\n\t"
-      "ds_read_u16 %14, %35 offset:%42\n\t"
-      "ds_read_u16 %15, %35 offset:%43\n\t"
-      "ds_read_u16 %16, %36 offset:%40\n\t"
-      "ds_read_u16 %17, %36 offset:%41\n\t"
-      "ds_read_u16 %18, %36 offset:%42\n\t"
-      "ds_read_u16 %19, %36 offset:%43\n\t"
-      "ds_read_u16 %20, %37 offset:%40\n\t"
-      "ds_read_u16 %21, %37 offset:%41\n\t"
-      "ds_read_u16 %22, %37 offset:%42\n\t"
-      "ds_read_u16 %23, %37 offset:%43\n\t"
-      "ds_read_u16 %24, %38 offset:%40\n\t"
-      "ds_read_u16 %25, %38 offset:%41\n\t"
-      "ds_read_u16 %26, %38 offset:%42\n\t"
-      "ds_read_u16 %27, %38 offset:%43\n\t"
-      "ds_read_u16 %28, %39 offset:%40\n\t"
-      "ds_read_u16 %29, %39 offset:%41\n\t"
-      "ds_read_u16 %30, %39 offset:%42\n\t"
-      "ds_read_u16 %31, %39 offset:%43\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
-        "=&v"(w[6]), "=&v"(w[7]), "=&v"(w[8]), "=&v"(w[9]), "=&v"(w[10]), "=&v"(w[11]),
-        "=&v"(w[12]), "=&v"(w[13]), "=&v"(w[14]), "=&v"(w[15]), "=&v"(w[16]), "=&v"(w[17]),
-        "=&v"(w[18]), "=&v"(w[19]), "=&v"(w[20]), "=&v"(w[21]), "=&v"(w[22]), "=&v"(w[23]),
-        "=&v"(w[24]), "=&v"(w[25]), "=&v"(w[26]), "=&v"(w[27]), "=&v"(w[28]), "=&v"(w[29]),
-        "=&v"(w[30]), "=&v"(w[31])
-      : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]),
-        "v"(va[7]), "n"(OFF), "n"(OFF + 256), "n"(OFF + 512), "n"(OFF + 768)
-      : "memory");
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    vt[j] = make_uint2(w[4 * j] | (w[4 * j + 1] << 16), w[4 * j + 2] | (w[4 * j + 3] << 16));
-}
-
 constexpr int kPfQ = 64;                          // queries per prefill block
 constexpr int kPfTileBytes = 2 * kSplit * D * 2;  // K then V of one staged 64-slot tile
 
@@ -1875,8 +1818,8 @@ constexpr int kPfTileBytes = 2 * kSplit * D * 2;  // K then V of one staged 64-s
 // weights). A query sees slots <= its own position (masked per lane); the
 // block reads tiles up to its largest position, the latest query tiles
 // first. K rows are staged rotated (chunk c of slot s at column (c + s) % 16)
-// and V rows by two chunks per four slots, so both operand reads are free of
-// bank conflicts.
+// and V rows by two chunks per slot (c + 2 (s % 8)); V^T operands come from
+// transpose reads, one per 16 dims and 16 slots.
 __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
   extern __shared__ __align__(16) unsigned char ring[];  // two staged tiles
   __shared__ int wave_pos[kBlock / kWave];
@@ -1920,7 +1863,7 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
   for (int u = 0; u < 4; ++u) {
     const int sl = 4 * u + (lane >> 4);
     kvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - sl) & 15) * 16);
-    vvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - 2 * u) & 15) * 16);
+    vvoff[u] = static_cast<uint32_t>(sl * 256 + (((lane & 15) - 2 * (sl & 7)) & 15) * 16);
   }
   auto stage = [&](int kt) {
     unsigned char* tb = ring + (kt & 1) * kPfTileBytes + wave * 4096;
@@ -1937,18 +1880,21 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
   if (nkt > 1) stage(1);
 
   // Operand addresses in tile buffer 0 (buffer 1 is kPfTileBytes further):
-  // K slot 16 mt + col, chunk 4 ks + quad, rotated by the slot; V^T dim
-  // 16 j + col of slots 16 mt + 4 quad + k, rotated by 2 quad.
+  // K slot 16 mt + col, chunk 4 ks + quad, rotated by the slot; for the V^T
+  // transpose reads, slot 16 mt + r (r = 4 quad + col / 4), dims
+  // 16 j + 4 (col % 4) .. + 3: 8 bytes of chunk 2 j + (col % 4) / 2, whose
+  // position the slot rotates by 2 (r % 8).
   const uint32_t ring_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)ring));
   uint32_t kaddr[4], vaddr[8];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     kaddr[ks] = ring_base + static_cast<uint32_t>(col * 256 + (((4 * ks + quad + col) & 15) * 16));
+  const int vr = 4 * quad + (col >> 2);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     vaddr[j] = ring_base + kSplit * D * 2 +
-               static_cast<uint32_t>(quad * 1024 + (((2 * j + (col >> 3) + 2 * quad) & 15) * 16) +
-                                     (col & 7) * 2);
+               static_cast<uint32_t>(vr * 256 + (((2 * j + ((col & 3) >> 1) + 2 * (vr & 7)) & 15) * 16) +
+                                     (col & 1) * 8);
 
   const float scale2 = a.scale * 1.4426950408889634f;  // log2(e) / sqrt(D)
   f32x4_t acc[8];
@@ -2014,10 +1960,10 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) va[j] = vaddr[j] + tb;
         uint2 vt[8];
-        if (mt == 0) read_vt_pf<0>(va, vt);
-        else if (mt == 1) read_vt_pf<4096>(va, vt);
-        else if (mt == 2) read_vt_pf<8192>(va, vt);
-        else read_vt_pf<12288>(va, vt);
+        if (mt == 0) read_vt_tr<0>(va, vt);
+        else if (mt == 1) read_vt_tr<4096>(va, vt);
+        else if (mt == 2) read_vt_tr<8192>(va, vt);
+        else read_vt_tr<12288>(va, vt);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
