@@ -1789,18 +1789,63 @@ __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
 
 // Operand reads of the prefill kernel's staged tiles (LDS-direct data, read
 // by inline asm: the compiler would wait for every load in flight before an
-// ordinary LDS read of such a buffer).
-// K operand of one 32-dim step for the four 16-slot M-tiles of a 64-slot tile.
-__device__ __forceinline__ void read_k_pf(uint32_t addr, u32x4 (&k)[4]) {
+// ordinary LDS read of such a buffer), issued without their waits: issue, run
+// other work, then a wait that names the registers as operands so no use of
+// them moves above it. K: one 32-dim step for the four 16-slot M-tiles of a
+// 64-slot tile; V^T: transpose reads as read_vt_tr.
+template <int OFF>
+__device__ __forceinline__ void issue_k_pf(uint32_t addr, u32x4 (&k)[4]) {
   asm volatile(
-      "ds_read_b128 %0, %4 offset:0\n\t"
-      "ds_read_b128 %1, %4 offset:4096\n\t"
-      "ds_read_b128 %2, %4 offset:8192\n\t"
-      "ds_read_b128 %3, %4 offset:12288\n\t"
-      "s_waitcnt lgkmcnt(0)"
+      "ds_read_b128 %0, %4 offset:%5\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %4 offset:%7\n\t"
+      "ds_read_b128 %3, %4 offset:%8"
       : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3])
-      : "v"(addr)
+      : "v"(addr), "n"(OFF), "n"(OFF + 4096), "n"(OFF + 8192), "n"(OFF + 12288)
       : "memory");
+}
+
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+template <int OFF>
+__device__ __forceinline__ void issue_vt_tr(const uint32_t (&va)[8], u32x2_t (&w)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %1, %9 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %2, %10 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %3, %11 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %4, %12 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %5, %13 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %6, %14 offset:%16\n\t"
+      "ds_read_b64_tr_b16 %7, %15 offset:%16"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+        "=&v"(w[6]), "=&v"(w[7])
+      : "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]),
+        "v"(va[7]), "n"(OFF)
+      : "memory");
+}
+
+__device__ __forceinline__ void wait_k16(u32x4 (&k)[4][4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(k[0][0]), "+v"(k[0][1]), "+v"(k[0][2]), "+v"(k[0][3]), "+v"(k[1][0]),
+                 "+v"(k[1][1]), "+v"(k[1][2]), "+v"(k[1][3]), "+v"(k[2][0]), "+v"(k[2][1]),
+                 "+v"(k[2][2]), "+v"(k[2][3]), "+v"(k[3][0]), "+v"(k[3][1]), "+v"(k[3][2]),
+                 "+v"(k[3][3])
+               :
+               : "memory");
+}
+
+__device__ __forceinline__ void wait_v32(u32x2_t (&w)[4][8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(w[0][0]), "+v"(w[0][1]), "+v"(w[0][2]), "+v"(w[0][3]), "+v"(w[0][4]),
+                 "+v"(w[0][5]), "+v"(w[0][6]), "+v"(w[0][7]), "+v"(w[1][0]), "+v"(w[1][1]),
+                 "+v"(w[1][2]), "+v"(w[1][3]), "+v"(w[1][4]), "+v"(w[1][5]), "+v"(w[1][6]),
+                 "+v"(w[1][7]), "+v"(w[2][0]), "+v"(w[2][1]), "+v"(w[2][2]), "+v"(w[2][3]),
+                 "+v"(w[2][4]), "+v"(w[2][5]), "+v"(w[2][6]), "+v"(w[2][7]), "+v"(w[3][0]),
+                 "+v"(w[3][1]), "+v"(w[3][2]), "+v"(w[3][3]), "+v"(w[3][4]), "+v"(w[3][5]),
+                 "+v"(w[3][6]), "+v"(w[3][7])
+               :
+               : "memory");
 }
 
 constexpr int kPfQ = 64;                          // queries per prefill block
@@ -1877,7 +1922,6 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
                                                vvoff[u], off, 0, 0);
   };
   if (nkt > 0) stage(0);
-  if (nkt > 1) stage(1);
 
   // Operand addresses in tile buffer 0 (buffer 1 is kPfTileBytes further):
   // K slot 16 mt + col, chunk 4 ks + quad, rotated by the slot; for the V^T
@@ -1902,27 +1946,41 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
   for (int j = 0; j < 8; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   for (int kt = 0; kt < nkt; ++kt) {
-    // This wave's part of tile kt has landed (tile kt + 1 may still be in
-    // flight), then everyone's.
-    if (kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // This wave's part of tile kt has landed; after the barrier everyone's
+    // has, and every wave has finished tile kt - 1, whose buffer tile kt + 1
+    // now takes (in flight during this tile's work).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
+    if (kt + 1 < nkt) stage(kt + 1);
     const int s0 = kt * kSplit;
     if (s0 <= wave_last) {  // wave-uniform: some slot of the tile is visible to the wave
       const uint32_t tb = static_cast<uint32_t>((kt & 1) * kPfTileBytes);
+      // All sixteen K fragments at once, then the scores.
+      u32x4 kf[4][4];
+      issue_k_pf<0>(kaddr[0] + tb, kf[0]);
+      issue_k_pf<0>(kaddr[1] + tb, kf[1]);
+      issue_k_pf<0>(kaddr[2] + tb, kf[2]);
+      issue_k_pf<0>(kaddr[3] + tb, kf[3]);
+      wait_k16(kf);
       f32x4_t st[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) st[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u32x4 kf[4];
-        read_k_pf(kaddr[ks] + tb, kf);
+      for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
-          st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mt]),
+          st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[ks][mt]),
                                                            __builtin_bit_cast(bf16x8_t, qf[ks]),
                                                            st[mt], 0, 0, 0);
-      }
+      // The V^T operands of the whole tile in flight during the softmax.
+      uint32_t va[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) va[j] = vaddr[j] + tb;
+      u32x2_t vw[4][8];
+      issue_vt_tr<0>(va, vw[0]);
+      issue_vt_tr<4096>(va, vw[1]);
+      issue_vt_tr<8192>(va, vw[2]);
+      issue_vt_tr<12288>(va, vw[3]);
       // Scores in base 2; slots past the query's position masked unless the
       // whole tile is visible to every query of the wave.
       const bool all_visible = s0 + kSplit - 1 <= wave_first;
@@ -1946,6 +2004,7 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] *= alpha;
       m = m_new;
+      uint4 phl[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         float p[4];
@@ -1955,25 +2014,17 @@ __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
         const uint2 pb = make_uint2(pack_bf2(p[0], p[1]), pack_bf2(p[2], p[3]));
         const uint2 pl = make_uint2(pack_bf2(p[0] - bf_lo(pb.x), p[1] - bf_hi(pb.x)),
                                     pack_bf2(p[2] - bf_lo(pb.y), p[3] - bf_hi(pb.y)));
-        const uint4 phl = make_uint4(pb.x, pb.y, pl.x, pl.y);
-        uint32_t va[8];
+        phl[mt] = make_uint4(pb.x, pb.y, pl.x, pl.y);
+      }
+      wait_v32(vw);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) va[j] = vaddr[j] + tb;
-        uint2 vt[8];
-        if (mt == 0) read_vt_tr<0>(va, vt);
-        else if (mt == 1) read_vt_tr<4096>(va, vt);
-        else if (mt == 2) read_vt_tr<8192>(va, vt);
-        else read_vt_tr<12288>(va, vt);
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, make_uint4(vt[j].x, vt[j].y, vt[j].x, vt[j].y)),
-              __builtin_bit_cast(bf16x8_t, phl), acc[j], 0, 0, 0);
-      }
+              __builtin_bit_cast(bf16x8_t, make_uint4(vw[mt][j].x, vw[mt][j].y, vw[mt][j].x, vw[mt][j].y)),
+              __builtin_bit_cast(bf16x8_t, phl[mt]), acc[j], 0, 0, 0);
     }
-    // Every wave has read tile kt before its buffer takes tile kt + 2.
-    lds_barrier();
-    if (kt + 2 < nkt) stage(kt + 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // O[query][dim 16 j + 4 quad + i] = acc[j][i] / (the four quads' sums).
