@@ -365,9 +365,10 @@ __device__ __forceinline__ bool split_coords(const AttnArgs& a, int& s, int& kvh
 
 // Agent-scope (sc1) loads: they miss the CU's L1, so they observe what other
 // CUs of this XCD stored to its L2.
-__device__ __forceinline__ float2 load_f2_sc1(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+__device__ __forceinline__ float2 load_f2_sc1(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                              uint32_t soff = 0) {
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 16);
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 16);
   return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
 }
 
@@ -378,10 +379,13 @@ template <int N>
 __device__ __forceinline__ void merge_row_short(__amdgpu_buffer_rsrc_t prs, __amdgpu_buffer_rsrc_t mrs,
                                                 int S, int lane, float& num_x, float& num_y,
                                                 float& den) {
-  const float2 ml = load_f2_sc1(mrs, lane * 8);
+  // One lane offset for every load; split u's D floats u * D * 4 bytes on
+  // (a constant offset, not one register per split).
+  const uint32_t lo = static_cast<uint32_t>(lane) * 8;
+  const float2 ml = load_f2_sc1(mrs, lo);
   float2 pv[N];
 #pragma unroll
-  for (int u = 0; u < N; ++u) pv[u] = load_f2_sc1(prs, (u * D + 2 * lane) * 4);
+  for (int u = 0; u < N; ++u) pv[u] = load_f2_sc1(prs, lo, u * D * 4);
   __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first wait
   const float M = wave_max(lane < S ? ml.x : -INFINITY);
   const float w = lane < S && ml.x != -INFINITY ? expf(ml.x - M) : 0.f;
@@ -410,9 +414,22 @@ __device__ __forceinline__ void merge_row_short(__amdgpu_buffer_rsrc_t prs, __am
 // visible in this L2: the merge still runs, and the mismatch count at byte
 // kXcdMismatchByte of the counters is incremented for the host to read.
 __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, int* last) {
+  // Everything the merge needs is computed before the arrival: the code after
+  // it runs on one block per pair, cold in its CU's instruction cache, so it
+  // is kept to the loads, the arithmetic and the store. The host takes this
+  // path for at most four rows (one per wave).
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int p = b * a.Hkv + kvh;
+  const int R = a.G * a.Q, S = a.splits;
+  const int r = wave < R ? wave : 0;
+  const long orow = static_cast<long>(p) * R + r;
+  const float* prow = a.part + orow * S * D;
+  const float* mrow = a.ml + orow * S * 2;
+  const int h = kvh * a.G + r / a.Q, t = r % a.Q;
+  bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st + 2 * lane;
+  asm volatile("" ::"s"(prow), "s"(mrow), "v"(dst), "s"(S));
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int p = b * a.Hkv + kvh;
   unsigned long long* cnt =
       reinterpret_cast<unsigned long long*>(a.done + static_cast<long>(p) * kCounterStride);
   if (threadIdx.x == 0) {
@@ -433,14 +450,9 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
   }
   __syncthreads();
   if (!*last) return;
-  // A wave-uniform row index keeps the row's descriptors in scalar registers.
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int R = a.G * a.Q, S = a.splits;
-  for (int r = wave; r < R; r += kBlock / kWave) {
-    const long orow = static_cast<long>(p) * R + r;
-    const __amdgpu_buffer_rsrc_t prs =
-        buffer_rsrc(a.part + orow * S * D, static_cast<uint32_t>(S) * D * 4);
-    const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(a.ml + orow * S * 2, static_cast<uint32_t>(S) * 8);
+  if (wave < R) {
+    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(prow, static_cast<uint32_t>(S) * D * 4);
+    const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(mrow, static_cast<uint32_t>(S) * 8);
     float nx, ny, den;
     // The fewest loads that cover the splits (each is a wave instruction
     // even where the descriptor returns zeros).
@@ -449,9 +461,7 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
     else if (S <= 24) merge_row_short<24>(prs, mrs, S, lane, nx, ny, den);
     else if (S <= 32) merge_row_short<32>(prs, mrs, S, lane, nx, ny, den);
     else merge_row_short<48>(prs, mrs, S, lane, nx, ny, den);
-    const int h = kvh * a.G + r / a.Q, t = r % a.Q;
-    bf16_t* dst = a.out + b * a.o_sb + h * a.o_sh + t * a.o_st;
-    *reinterpret_cast<uint32_t*>(dst + 2 * lane) = pack_bf2(nx / den, ny / den);
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf2(nx / den, ny / den);
   }
   if (threadIdx.x == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
