@@ -340,6 +340,22 @@ __device__ __forceinline__ void prefetch_next(const AttnArgs& a, unsigned char* 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// The kernel arguments the staged attention kernels read before their first
+// vector load, named as scalar operands at entry: the compiler then issues
+// their scalar loads as one round instead of one dependent round per use
+// (four rounds, each a cold scalar-cache miss, before the first K/V load).
+template <bool FUSED>
+__device__ __forceinline__ void preload_args(const AttnArgs& a) {
+  asm volatile("" ::"s"(a.pf), "s"(a.attn_blocks), "s"(a.done), "s"(a.splits), "s"(a.split),
+               "s"(a.Hkv), "s"(a.B), "s"(a.G), "s"(a.cap), "s"(a.keys), "s"(a.values),
+               "s"(a.pos));
+  if constexpr (FUSED)
+    asm volatile("" ::"s"(a.qkv), "s"(a.qkv_sb), "s"(a.k_off), "s"(a.v_off), "s"(a.qg),
+                 "s"(a.kg), "s"(a.cos), "s"(a.sin));
+  else
+    asm volatile("" ::"s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.q_st), "s"(a.Q));
+}
+
 // Block coordinates (split s, kv head, batch). With the in-kernel merge the
 // grid is one-dimensional: block L runs on XCD L % 8 (round-robin dispatch;
 // on 1, 2 or 4 XCDs blocks with equal L % 8 still share one), and the splits
@@ -1119,6 +1135,7 @@ template <int ROWS, int PRO, int RING>
 __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  preload_args<FUSED>(a);
   if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
     prefetch_next(a, ring);
     return;
@@ -1463,6 +1480,7 @@ template <int ROWS, int PRO, int RING>
 __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
+  preload_args<FUSED>(a);
   if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
     prefetch_next(a, ring);
     return;
