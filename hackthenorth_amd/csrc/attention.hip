@@ -177,6 +177,12 @@ struct RopeArgs {
 // head (a 16-lane row must run whole) and store nothing. The launch keeps
 // tokens * chunks below 2^31.
 __global__ __launch_bounds__(kBlock) void norm_rope_cache_kernel(RopeArgs a) {
+  // Arguments in scalar registers at entry: one round of scalar loads.
+  asm volatile("" ::"s"(a.q), "s"(a.q_sb), "s"(a.q_st), "s"(a.k), "s"(a.k_sb), "s"(a.k_st),
+               "s"(a.v), "s"(a.v_sb), "s"(a.v_st), "s"(a.qg), "s"(a.kg), "s"(a.pos));
+  asm volatile("" ::"s"(a.cos), "s"(a.sin), "s"(a.rope_st), "s"(a.rope_rows), "s"(a.keys),
+               "s"(a.values), "s"(a.cap), "s"(a.B), "s"(a.T), "s"(a.Hq), "s"(a.Hkv));
+  asm volatile("" ::"s"(a.q_eps), "s"(a.k_eps), "s"(a.rope_by_pos), "s"(a.out_q), "s"(a.out_k));
   const int lane = threadIdx.x & 63, e = lane & 15, row = lane >> 4;
   const unsigned qc = (a.Hq + 15) >> 4, chunks = qc + ((a.Hkv + 15) >> 4);
   const unsigned w = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -555,6 +561,7 @@ enum Prologue { PRO_NONE = 0, PRO_ROW = 1, PRO_BY_POSITION = 2 };
 template <int ROWS, int PRO, int TILES>
 __global__ __launch_bounds__(kBlock) void attention_partial(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
+  preload_args<FUSED>(a);
   constexpr int SPLIT = kSplit * TILES;
   constexpr int kQLoads = kMaxRows * (D / 2) / kBlock;  // q pairs per thread, unfused
   __shared__ uint32_t qs[kMaxRows * D / 2];  // query rows as bf16 pairs
@@ -902,6 +909,7 @@ __device__ __forceinline__ void stream_tile(const AttnArgs& a, KVTile& t, int tb
 template <int ROWS, int PRO>
 __global__ __launch_bounds__(kBlock) void attention_stream(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
+  preload_args<FUSED>(a);
   __shared__ uint32_t qs[kMaxRows * D / 2];
   __shared__ float sc[2][ROWS * kSplit];
   __shared__ float accr[4 * ROWS * D];
@@ -1894,6 +1902,7 @@ constexpr int kPfTileBytes = 2 * kSplit * D * 2;  // K then V of one staged 64-s
 // and V rows by two chunks per slot (c + 2 (s % 8)); V^T operands come from
 // transpose reads, one per 16 dims and 16 slots.
 __global__ __launch_bounds__(kBlock) void attention_prefill(AttnArgs a) {
+  preload_args<false>(a);
   extern __shared__ __align__(16) unsigned char ring[];  // two staged tiles
   __shared__ int wave_pos[kBlock / kWave];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -2080,6 +2089,8 @@ struct MergeArgs {
 };
 
 __global__ __launch_bounds__(kBlock) void attention_merge(MergeArgs a) {
+  asm volatile("" ::"s"(a.part), "s"(a.ml), "s"(a.out), "s"(a.o_sb), "s"(a.o_sh), "s"(a.o_st),
+               "s"(a.splits), "s"(a.Hq), "s"(a.Q));
   const float* __restrict__ part = a.part;
   const float* __restrict__ ml = a.ml;
   const int splits = a.splits;

@@ -87,10 +87,20 @@ __device__ __forceinline__ void store_out(const RowsArgs& a, int m, int n, float
   a.y[m * a.y_rs + n] = static_cast<bf16_t>(f2bf(out));
 }
 
+// The fields every row kernel reads early, in scalar registers at entry: one
+// round of scalar loads instead of one per dependent use.
+__device__ __forceinline__ void preload_rows(const RowsArgs& a) {
+  asm volatile("" ::"s"(a.x), "s"(a.x_rs), "s"(a.w), "s"(a.res), "s"(a.res_rs), "s"(a.y),
+               "s"(a.y_rs), "s"(a.part), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.KS),
+               "s"(a.steps_per_split));
+}
+
 constexpr int kPitch = 144;  // bytes per staged 64-element weight row (+16: conflict-free reads)
 
 template <int MT, int S, int EPI, int W, bool NORM>
 __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
+  preload_rows(a);
+  if constexpr (NORM) asm volatile("" ::"s"(a.xgain), "s"(a.xeps));
   __shared__ float red[W][MT][S][kStrip * 16];
   __shared__ uint64_t best[EPI == HTN_EPI_ARGMAX ? MT * 16 : 1][kStrip];
   __shared__ __align__(16) unsigned char tile[W][16 * kPitch];
@@ -330,6 +340,7 @@ __global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
 // Sum of the K-split partials in split order, then the epilogue.
 template <int S, int EPI>
 __global__ __launch_bounds__(kBlock) void gemm_rows_finish(RowsArgs a) {
+  preload_rows(a);
   const long o = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
   if (o >= static_cast<long>(a.M) * a.N) return;
   const int m = static_cast<int>(o / a.N), n = static_cast<int>(o % a.N);
@@ -352,6 +363,8 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_finish(RowsArgs a) {
 // reduction), so `normed` is bit-identical to running that norm on y, and
 // every thread normalises its vectors from LDS.
 __global__ __launch_bounds__(kBlock) void gemm_rows_finish_norm(RowsArgs a) {
+  preload_rows(a);
+  asm volatile("" ::"s"(a.ngain), "s"(a.neps), "s"(a.normed));
   __shared__ uint4 ys[8192 / 8];  // the row of y, up to 8192 columns
   __shared__ float inv_s;
   const int tid = threadIdx.x;
@@ -406,6 +419,7 @@ __global__ __launch_bounds__(kBlock) void gemm_rows_finish_norm(RowsArgs a) {
 // Per-row argmax over the strips' keys.
 __global__ __launch_bounds__(kBlock) void gemm_rows_argmax(const uint64_t* __restrict__ keys,
                                                           int strips, int M, int64_t* tokens) {
+  asm volatile("" ::"s"(keys), "s"(strips), "s"(M), "s"(tokens));
   __shared__ uint64_t wbest[4];
   const int m = blockIdx.x;
   uint64_t b = 0;
@@ -442,6 +456,7 @@ constexpr int kUI = 2;         // steps in flight per wave
 
 template <int MT, int W>
 __global__ __launch_bounds__(W * 64) void gemm_rows_interleaved(RowsArgs a) {
+  preload_rows(a);
   __shared__ float red[W][MT][4][16 * 16];  // [wave][row tile][tile t, gate/up][row][col]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int strip = blockIdx.x, ks = blockIdx.y;

@@ -149,6 +149,9 @@ __device__ __forceinline__ void store_tile(const TileArgs& a, const f32x4_t (&ac
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
+  // Arguments in scalar registers at entry: one round of scalar loads.
+  asm volatile("" ::"s"(a.x), "s"(a.x_rs), "s"(a.w), "s"(a.res), "s"(a.res_rs), "s"(a.y),
+               "s"(a.y_rs), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.mtiles), "s"(a.ntiles));
   extern __shared__ __align__(16) unsigned char lds[];  // two stages of x and weight tiles
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -117,6 +117,7 @@ __device__ __forceinline__ void argmax_block(const GemvArgs& a, uint64_t best, u
 // token and (decode step) advances the position.
 __global__ __launch_bounds__(kBlock) void argmax_finish(const uint64_t* __restrict__ partial, int n,
                                                        int64_t* token_out, int64_t* position_inc) {
+  asm volatile("" ::"s"(partial), "s"(n), "s"(token_out), "s"(position_inc));
   __shared__ uint64_t keys[4];
   uint64_t best = 0;
   for (int i = threadIdx.x; i < n; i += kBlock) best = partial[i] > best ? partial[i] : best;
@@ -197,6 +198,13 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   bf16_t* xs = reinterpret_cast<bf16_t*>(smem);   // normalised x (NORM only)
   // The wave index is uniform: readfirstlane keeps row addresses in SGPRs.
   const int lane = threadIdx.x & 63;
+  // Every kernel argument (and the grid size, a hidden argument) in scalar
+  // registers before anything uses them: one round of scalar loads instead
+  // of two.
+  asm volatile("" ::"s"(a.w), "s"(a.x), "s"(a.y), "s"(a.n), "s"(a.k), "s"(gridDim.x));
+  if constexpr (NORM) asm volatile("" ::"s"(a.gain), "s"(a.eps));
+  if constexpr (EPI == EPI_RESIDUAL) asm volatile("" ::"s"(a.res));
+  if constexpr (WF != WF_BF16) asm volatile("" ::"s"(a.scale));
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kv = a.k / EPV;
   const int chunks = (kv + 63) >> 6;
@@ -204,11 +212,6 @@ __global__ __launch_bounds__(kBlock) void gemv_vec(GemvArgs a) {
   const long stride = static_cast<long>(gridDim.x) * 4;
   long grp = static_cast<long>(blockIdx.x) * 4 + wave;
   const int kv8 = a.k >> 3;
-  // Every kernel argument in scalar registers before the first branch: one
-  // round of scalar loads instead of two.
-  asm volatile("" ::"s"(a.w), "s"(a.x), "s"(a.y), "s"(a.n), "s"(a.k));
-  if constexpr (NORM) asm volatile("" ::"s"(a.gain), "s"(a.eps));
-  if constexpr (EPI == EPI_RESIDUAL) asm volatile("" ::"s"(a.res));
 
   // RMSNorm operands first: vector loads complete in issue order, so loading
   // x and the gain ahead of the weights lets the prologue start as soon as

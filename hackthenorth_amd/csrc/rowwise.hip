@@ -24,6 +24,9 @@ __global__ __launch_bounds__(kBlock) void norm_rows_vec(const bf16_t* __restrict
                                                         bf16_t* __restrict__ summed,
                                                         bf16_t* __restrict__ out, long rows,
                                                         int cols, float eps) {
+  // Arguments in scalar registers before their first use: one round of loads.
+  asm volatile("" ::"s"(x), "s"(x_stride), "s"(r), "s"(gain), "s"(summed), "s"(out), "s"(rows),
+               "s"(cols), "s"(eps));
   constexpr int kMaxVec = 16;  // up to 8192 columns per row
   const int lane = threadIdx.x & 63;
   const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -105,6 +108,7 @@ constexpr int kSwigluPieces = 2;
 __global__ __launch_bounds__(kBlock) void swiglu_vec(const bf16_t* __restrict__ g, long gs,
                                                      const bf16_t* __restrict__ u, long us,
                                                      bf16_t* __restrict__ out, long rows, int cols) {
+  asm volatile("" ::"s"(g), "s"(gs), "s"(u), "s"(us), "s"(out), "s"(rows), "s"(cols));
   const unsigned nv = static_cast<unsigned>(cols) >> 3;
   const unsigned total = static_cast<unsigned>(rows) * nv;
   const unsigned base = blockIdx.x * (kBlock * kSwigluPieces) + threadIdx.x;
@@ -196,7 +200,14 @@ __device__ __forceinline__ void embed_wave(const EmbedJob& j, long w) {
   }
 }
 
+// A job's fields in scalar registers before their first use: one round of
+// scalar loads instead of one per dependent use.
+__device__ __forceinline__ void preload_job(const EmbedJob& j) {
+  asm volatile("" ::"s"(j.ids), "s"(j.count), "s"(j.table), "s"(j.vocab), "s"(j.hidden), "s"(j.out));
+}
+
 __global__ __launch_bounds__(kBlock) void embed_vec(EmbedJob j) {
+  preload_job(j);
   embed_wave(j, static_cast<long>(blockIdx.x) * (kBlock / kWave) +
                     __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
 }
@@ -204,6 +215,9 @@ __global__ __launch_bounds__(kBlock) void embed_vec(EmbedJob j) {
 // Two gathers in one launch (the decode step's token row and RoPE row):
 // blocks below split take job a, the rest job b.
 __global__ __launch_bounds__(kBlock) void embed_pair(EmbedJob a, EmbedJob b, unsigned split) {
+  preload_job(a);
+  preload_job(b);
+  asm volatile("" ::"s"(split));
   const long w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (blockIdx.x < split) embed_wave(a, static_cast<long>(blockIdx.x) * (kBlock / kWave) + w);
   else embed_wave(b, static_cast<long>(blockIdx.x - split) * (kBlock / kWave) + w);
