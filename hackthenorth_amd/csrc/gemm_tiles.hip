@@ -184,7 +184,7 @@ struct Stage {
 template <int TM>
 __device__ __forceinline__ void stage_tiles(unsigned char* lds, int ks, int wave,
                                             __amdgpu_buffer_rsrc_t xrs, __amdgpu_buffer_rsrc_t wrs,
-                                            const uint32_t (&xoff)[TM / 32],
+                                            const uint32_t (&xoff)[4],
                                             const uint32_t (&woff)[4]) {
   unsigned char* st = lds + (ks & 1) * Stage<TM>::kBytes;
   const uint32_t ko = static_cast<uint32_t>(ks) * kTk * 2u;
@@ -200,10 +200,6 @@ __device__ __forceinline__ void stage_tiles(unsigned char* lds, int ks, int wave
 
 template <int EPI, int TM>
 __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  // (Device pass only: with the x-tile height a template parameter, the host
-  // pass cannot substitute the buffer-descriptor code and would drop the
-  // kernel's launch stub without a diagnostic.)
   // Arguments in scalar registers at entry: one round of scalar loads.
   asm volatile("" ::"s"(a.x), "s"(a.x_rs), "s"(a.w), "s"(a.res), "s"(a.res_rs), "s"(a.y),
                "s"(a.y_rs), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.mtiles), "s"(a.ntiles));
@@ -250,7 +246,7 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
   }
   const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(a.w + (wrows > 0 ? wbase : 0) * a.K,
                                                   static_cast<uint32_t>(wrows * a.K * 2));
-  uint32_t xoff[TM / 32], woff[4];
+  uint32_t xoff[4], woff[4];  // x offsets: the first TM / 32 are used
 #pragma unroll
   for (int u = 0; u < XR / 8; ++u) {
     const int r = XR * wave + 8 * u + lr;  // x tile row
@@ -325,7 +321,6 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
   }
 
   store_tile<EPI, NT>(a, acc, m0 + (TM / 2) * wm, SW ? n0 + 32 * wn : n0 + 64 * wn, col, quad);
-#endif
 }
 
 template <int EPI, int TM>
