@@ -53,7 +53,8 @@ SIGNATURES = {
     "htn_gemm_rows_scratch_bytes": [_I64, _I64, _I64, _I, _I],
     "htn_gemm_rows": [_P, _I64, _P, _F, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P,
                       _P],
-    "htn_gemm_tiles": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P],
+    "htn_gemm_tiles_scratch_bytes": [_I64, _I64, _I64, _I],
+    "htn_gemm_tiles": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P],
     "htn_gemm_rows_residual_norm": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F,
                                     _P, _P, _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],
@@ -76,6 +77,7 @@ SIGNATURES = {
     "htn_attention_merge_in_kernel": [],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
+            "htn_gemm_tiles_scratch_bytes": _I64,
             "htn_gate_up_swiglu_scratch_bytes": _I64, "htn_stream_read_blocks": _I64,
             "htn_head_scratch_capacity": _I64}
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX, EPI_RESIDUAL_NORM = 0, 1, 2, 3, 4

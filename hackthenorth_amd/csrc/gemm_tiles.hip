@@ -22,6 +22,11 @@
 //  * when the 128-row grid would leave CUs without a block (short prompts),
 //    tiles take 64 x rows (each wave a 32 x 64 part), twice the blocks over
 //    the same weight tiles;
+//  * when the tiles fill at most half of the blocks the CUs hold at once
+//    (prompts of a few hundred rows; the K-long down projection most of
+//    all), each tile's k range splits over up to 8 blocks, as many as fit in
+//    one round of resident blocks; they store fp32 partial sums and a second
+//    launch adds them in split order and applies the epilogue;
 //  * blocks are laid out XCD-major: the blocks of one weight tile share an
 //    XCD (block L runs on XCD L % 8), so its L2 serves the tile to all of them.
 //
@@ -47,7 +52,13 @@ struct TileArgs {
   bf16_t* y; long y_rs;
   int M, N, K;        // N: output columns (gate columns for SwiGLU)
   int mtiles, ntiles; // output tiles along M and N
+  int ksplit, steps;  // k splits per tile, 64-wide k steps per split
+  float* part;        // K-split partial sums [ksplit][M][part_rs]
+  long part_rs;       // round4(N), twice that for SwiGLU (gate, then up sums)
 };
+
+constexpr int kMinSplitSteps = 16;    // k steps each split keeps at least
+constexpr int kMaxSplit = 8;
 
 // Eight 16-byte operand fragments in one asm block: LDS-direct data is read by
 // inline asm (the compiler would wait for every load in flight before an
@@ -172,6 +183,27 @@ __device__ __forceinline__ void store_tile(const TileArgs& a, const f32x4_t (&ac
   }
 }
 
+// K-split epilogue: the block's fp32 sums of its k range, unrounded, at
+// part[(s M + m) part_rs + c], c = the output column, or for SwiGLU c = n for
+// the gate sums and part_rs / 2 + n for the up sums of output column n. The
+// four columns of a lane end before round4(N), so every store is whole.
+template <bool SW, int NT>
+__device__ __forceinline__ void store_part(const TileArgs& a, const f32x4_t (&acc)[4][NT], int s,
+                                           int mb, int nb, int col, int quad) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int m = mb + 16 * t + col;
+    if (m >= a.M) continue;
+    float* row = a.part + (static_cast<long>(s) * a.M + m) * a.part_rs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = nb + 16 * (SW ? (i & 1) : i) + 4 * quad;
+      if (n >= a.N) continue;
+      *reinterpret_cast<f32x4_t*>(row + (SW && i >= 2 ? a.part_rs / 2 : 0) + n) = acc[i][t];
+    }
+  }
+}
+
 // Bytes of one staged k step: the x tile (TM rows) and the weight tile (128
 // rows), 128 bytes per row.
 template <int TM>
@@ -202,7 +234,8 @@ template <int EPI, int TM>
 __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
   // Arguments in scalar registers at entry: one round of scalar loads.
   asm volatile("" ::"s"(a.x), "s"(a.x_rs), "s"(a.w), "s"(a.res), "s"(a.res_rs), "s"(a.y),
-               "s"(a.y_rs), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.mtiles), "s"(a.ntiles));
+               "s"(a.y_rs), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.mtiles), "s"(a.ntiles),
+               "s"(a.ksplit), "s"(a.steps), "s"(a.part), "s"(a.part_rs));
   extern __shared__ __align__(16) unsigned char lds[];  // two stages of x and weight tiles
   constexpr int NT = TM / 32;        // 16-row x tiles per wave (4 or 2)
   constexpr int XR = TM / 4;         // x rows each wave stages (32 or 16)
@@ -213,9 +246,11 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
   const int wm = wave & 1, wn = wave >> 1;  // this wave's TM / 2 x rows, 64 weight rows
   const int col = lane & 15, quad = lane >> 4;
   // XCD-major layout: block L on XCD L % 8 takes weight tile
-  // nt = (L / 8 / mtiles) * 8 + L % 8 and row tile (L / 8) % mtiles.
-  const int L = blockIdx.x, j = L >> 3;
-  const int nt = (j / a.mtiles) * 8 + (L & 7), mt = j - (j / a.mtiles) * a.mtiles;
+  // nt = (L / 8 / (mtiles ksplit)) * 8 + L % 8, row tile (L / 8) % mtiles and
+  // k split (L / 8 / mtiles) % ksplit.
+  const int L = blockIdx.x, j = L >> 3, per = a.mtiles * a.ksplit;
+  const int g = j / per, q = j - g * per, s = q / a.mtiles;
+  const int nt = g * 8 + (L & 7), mt = q - s * a.mtiles;
   if (nt >= a.ntiles) return;
   const int m0 = mt * TM;
   // Weight rows of the tile: rows n0 .. n0 + 127, or for SwiGLU 64 output
@@ -284,14 +319,15 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
     for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nk = a.K / kTk;
-  stage_tiles<TM>(lds, 0, wave, xrs, wrs, xoff, woff);
-  for (int ks = 0; ks < nk; ++ks) {
+  const int k0 = s * a.steps, k1 = nk < k0 + a.steps ? nk : k0 + a.steps;
+  stage_tiles<TM>(lds, k0, wave, xrs, wrs, xoff, woff);
+  for (int ks = k0; ks < k1; ++ks) {
     // This wave's part of step ks has landed; after the barrier everyone's
     // has, and every wave has finished step ks - 1, whose stage step ks + 1
     // now takes (in flight during this step's multiplies).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier_t();
-    if (ks + 1 < nk) stage_tiles<TM>(lds, ks + 1, wave, xrs, wrs, xoff, woff);
+    if (ks + 1 < k1) stage_tiles<TM>(lds, ks + 1, wave, xrs, wrs, xoff, woff);
     const uint32_t so = static_cast<uint32_t>((ks & 1) * kStage);
     if constexpr (NT == 4) {
       u32x4 f0[8], f1[8];
@@ -320,32 +356,114 @@ __global__ __launch_bounds__(256) void gemm_tiles_kernel(TileArgs a) {
     }
   }
 
-  store_tile<EPI, NT>(a, acc, m0 + (TM / 2) * wm, SW ? n0 + 32 * wn : n0 + 64 * wn, col, quad);
+  const int mb = m0 + (TM / 2) * wm, nb = SW ? n0 + 32 * wn : n0 + 64 * wn;
+  if (a.ksplit > 1)
+    store_part<SW, NT>(a, acc, s, mb, nb, col, quad);
+  else
+    store_tile<EPI, NT>(a, acc, mb, nb, col, quad);
+}
+
+// K-split sum + epilogue: thread i takes output columns 4 (i % (part_rs' / 4))
+// .. + 3 of row i / (part_rs' / 4) (part_rs' = round4(N)), adds the splits'
+// partials in split order and rounds as store_tile does.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_tiles_finish(TileArgs a) {
+  asm volatile("" ::"s"(a.res), "s"(a.res_rs), "s"(a.y), "s"(a.y_rs), "s"(a.M), "s"(a.N),
+               "s"(a.ksplit), "s"(a.part), "s"(a.part_rs));
+  constexpr bool SW = EPI == HTN_EPI_SWIGLU;
+  const long n4 = (SW ? a.part_rs / 2 : a.part_rs) / 4;
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long m = i / n4;
+  if (m >= a.M) return;
+  const int n = static_cast<int>(i - m * n4) * 4;
+  const long stride = static_cast<long>(a.M) * a.part_rs;
+  const float* p = a.part + m * a.part_rs + n;
+  f32x4_t g = *reinterpret_cast<const f32x4_t*>(p), u{};
+  if (SW) u = *reinterpret_cast<const f32x4_t*>(p + a.part_rs / 2);
+  for (int s = 1; s < a.ksplit; ++s) {
+    g += *reinterpret_cast<const f32x4_t*>(p + s * stride);
+    if (SW) u += *reinterpret_cast<const f32x4_t*>(p + s * stride + a.part_rs / 2);
+  }
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (SW)
+      o[e] = silu_bf(round_bf(g[e])) * round_bf(u[e]);
+    else if (EPI == HTN_EPI_RESIDUAL)
+      o[e] = round_bf(g[e]) + (n + e < a.N ? bf2f(a.res[m * a.res_rs + n + e]) : 0.f);
+    else
+      o[e] = g[e];
+  }
+  bf16_t* dst = a.y + m * a.y_rs + n;
+  if (n + 4 <= a.N) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+  } else {
+    for (int e = 0; e < 4 && n + e < a.N; ++e) dst[e] = static_cast<bf16_t>(f2bf(o[e]));
+  }
+}
+
+// Launch shape: the row tile (128, or 64 when the 128-row grid would leave
+// CUs without a block: twice the blocks over the same weight tiles; 8B
+// 256-token prefill 14.9 -> 13.9 ms, at a full first wave of 128-row blocks
+// the 64-row tiles measured slower) and the k split.
+struct TilePlan {
+  int tm, ksplit, steps;
+  long blocks, part_rs;
+};
+
+TilePlan plan_tiles(long rows, long n, long k, int epilogue) {
+  const bool sw = epilogue == HTN_EPI_SWIGLU;
+  const long cols = (((sw ? (n + 63) / 64 : (n + kTn - 1) / kTn) + 7) / 8) * 8;
+  const long cus = device_cus();
+  TilePlan p{};
+  p.tm = cols * ((rows + 127) / 128) < cus ? 64 : 128;
+  const long base = cols * ((rows + p.tm - 1) / p.tm);
+  const long nk = k / kTk;
+  // Blocks resident at once: 64-row tiles take 48 KB of the CU's 160 KB of
+  // LDS (three blocks), 128-row tiles 64 KB (two). A split that overflows
+  // one round of them measured slower (8B QKV at 1024 rows: 384 -> 768
+  // blocks of 128 rows, 74 -> 87 us).
+  const long slots = cus * (p.tm == 64 ? 3 : 2);
+  long ks = 1;
+  if (2 * base <= slots) {
+    ks = slots / base;
+    if (ks > nk / kMinSplitSteps) ks = nk / kMinSplitSteps;
+    if (ks > kMaxSplit) ks = kMaxSplit;
+    if (ks < 1) ks = 1;
+  }
+  p.steps = static_cast<int>((nk + ks - 1) / ks);
+  p.ksplit = static_cast<int>((nk + p.steps - 1) / p.steps);
+  p.blocks = base * p.ksplit;
+  p.part_rs = (sw ? 2 : 1) * ((n + 3) / 4 * 4);
+  return p;
+}
+
+long tiles_scratch_bytes(const TilePlan& p, long rows) {
+  return p.ksplit > 1 ? static_cast<long>(p.ksplit) * rows * p.part_rs * 4 : 0;
 }
 
 template <int EPI, int TM>
-int launch_tiles(TileArgs& a, hipStream_t st) {
+int launch_tiles(TileArgs& a, long blocks, hipStream_t st) {
   const size_t lds = 2 * static_cast<size_t>(Stage<TM>::kBytes);
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&gemm_tiles_kernel<EPI, TM>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   (void)attr;  // a refused size surfaces as a launch error
   a.mtiles = static_cast<int>((a.M + TM - 1) / TM);
-  const long blocks = static_cast<long>((a.ntiles + 7) / 8) * 8 * a.mtiles;
   hipLaunchKernelGGL((gemm_tiles_kernel<EPI, TM>), dim3(static_cast<unsigned>(blocks)), dim3(256),
                      lds, st, a);
   return launch_status();
 }
 
-// 128-row tiles when their grid gives every CU a block; fewer rows (short
-// prompts) take 64-row tiles, twice the blocks over the same weight tiles
-// (8B: 256-token prefill 14.9 -> 13.9 ms; at a full first wave of 128-row
-// blocks the 64-row tiles measured slower).
 template <int EPI>
-int launch_tiles_for(TileArgs& a, hipStream_t st) {
-  const long blocks128 = static_cast<long>((a.ntiles + 7) / 8) * 8 * ((a.M + 127) / 128);
-  if (blocks128 < device_cus()) return launch_tiles<EPI, 64>(a, st);
-  return launch_tiles<EPI, 128>(a, st);
+int launch_tiles_for(TileArgs& a, const TilePlan& p, hipStream_t st) {
+  const int rc = p.tm == 64 ? launch_tiles<EPI, 64>(a, p.blocks, st)
+                            : launch_tiles<EPI, 128>(a, p.blocks, st);
+  if (rc != HTN_OK || a.ksplit == 1) return rc;
+  const long groups = static_cast<long>(a.M) * ((a.N + 3) / 4);
+  hipLaunchKernelGGL((gemm_tiles_finish<EPI>), dim3(static_cast<unsigned>((groups + 255) / 256)),
+                     dim3(256), 0, st, a);
+  return launch_status();
 }
 
 }  // namespace
@@ -353,9 +471,17 @@ int launch_tiles_for(TileArgs& a, hipStream_t st) {
 
 using namespace htn;
 
+extern "C" int64_t htn_gemm_tiles_scratch_bytes(int64_t rows, int64_t n, int64_t k,
+                                                int epilogue) {
+  if (rows <= 0 || n <= 0 || k <= 0 || k % kTk) return 0;
+  if (epilogue != HTN_EPI_STORE && epilogue != HTN_EPI_RESIDUAL && epilogue != HTN_EPI_SWIGLU)
+    return 0;
+  return tiles_scratch_bytes(plan_tiles(rows, n, k, epilogue), rows);
+}
+
 extern "C" int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, int64_t n,
                               int64_t k, int64_t rows, int epilogue, const void* residual,
-                              int64_t res_stride, void* y, int64_t y_stride,
+                              int64_t res_stride, void* y, int64_t y_stride, void* scratch,
                               htn_stream_t stream) {
   if (!x || !w || !y || rows <= 0 || n <= 0 || k <= 0) return HTN_EINVAL;
   if (epilogue != HTN_EPI_STORE && epilogue != HTN_EPI_RESIDUAL && epilogue != HTN_EPI_SWIGLU)
@@ -378,9 +504,20 @@ extern "C" int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, in
   a.M = static_cast<int>(rows); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
   hipStream_t st = static_cast<hipStream_t>(stream);
   a.ntiles = static_cast<int>(epilogue == HTN_EPI_SWIGLU ? (n + 63) / 64 : (n + kTn - 1) / kTn);
+  if (!aligned16(scratch)) return HTN_EUNSUPPORTED;
+  TilePlan p = plan_tiles(rows, n, k, epilogue);
+  if (!scratch) {  // no scratch: every tile sums its whole k range
+    p.blocks /= p.ksplit;
+    p.ksplit = 1;
+    p.steps = static_cast<int>(k / kTk);
+  }
+  a.ksplit = p.ksplit;
+  a.steps = p.steps;
+  a.part = static_cast<float*>(scratch);
+  a.part_rs = p.part_rs;
   switch (epilogue) {
-    case HTN_EPI_STORE: return launch_tiles_for<HTN_EPI_STORE>(a, st);
-    case HTN_EPI_RESIDUAL: return launch_tiles_for<HTN_EPI_RESIDUAL>(a, st);
-    default: return launch_tiles_for<HTN_EPI_SWIGLU>(a, st);
+    case HTN_EPI_STORE: return launch_tiles_for<HTN_EPI_STORE>(a, p, st);
+    case HTN_EPI_RESIDUAL: return launch_tiles_for<HTN_EPI_RESIDUAL>(a, p, st);
+    default: return launch_tiles_for<HTN_EPI_SWIGLU>(a, p, st);
   }
 }

@@ -28,9 +28,12 @@ def _tiles(x, weight, n, epilogue, residual=None, gain=None, eps=1e-6):
                   float(eps), _lib.stream(x.device))
         x = xn
     out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    nbytes = _lib.load().htn_gemm_tiles_scratch_bytes(rows, n, k, epilogue)
+    scratch = torch.empty((nbytes + 15) // 16, 4, dtype=torch.float32, device=x.device) \
+        if nbytes > 0 else None
     _lib.call("htn_gemm_tiles", _lib.ptr(x), x.stride(0), _lib.ptr(weight), n, k, rows, epilogue,
               _lib.ptr(residual), residual.stride(0) if residual is not None else 0,
-              _lib.ptr(out), out.stride(0), _lib.stream(x.device))
+              _lib.ptr(out), out.stride(0), _lib.ptr(scratch), _lib.stream(x.device))
     return out
 
 

@@ -250,7 +250,15 @@ int htn_gemm_rows_residual_norm(const void* x, int64_t x_stride, const void* w, 
  * forward (prefill.py:6-26 -> DecodeState.prefill, decode.py:156-166). */
 int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, int64_t n, int64_t k,
                    int64_t rows, int epilogue, const void* residual, int64_t res_stride, void* y,
-                   int64_t y_stride, htn_stream_t stream);
+                   int64_t y_stride, void* scratch, htn_stream_t stream);
+
+/* Scratch bytes htn_gemm_tiles uses for these sizes (0: none). When the tile
+ * grid alone fills at most half of the blocks the CUs hold at once (prompts
+ * of a few hundred rows), each tile's k range splits over up to 8 blocks whose fp32
+ * partial sums go to `scratch` (16-byte aligned) and a second launch adds
+ * them in split order; with scratch NULL every tile sums its whole k range.
+ * The two orders of the fp32 sums may round an output 1 bf16 ulp apart. */
+int64_t htn_gemm_tiles_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue);
 
 /* SwiGLU of `rows` (1..32) activation rows x[m, :k] (row stride x_stride)
  * by the interleaved K-major weight w[k, 2 * width] (row-major, w[k, 2i] the

@@ -95,6 +95,58 @@ def test_tiled_projection_rows_match_oracle(m, n, k):
                                Q.silu_mul(gu[:, :n], gu[:, n:]).float(), atol=2e-2, rtol=2e-2)
 
 
+def _tiles_abi(x, w, n, epilogue, residual=None, split=True):
+    """htn_gemm_tiles through the C-ABI, with its planned k split (scratch
+    given) or each tile over its whole k range (scratch NULL)."""
+    from hackthenorth_amd import _lib
+    rows, k = x.shape
+    nbytes = _lib.load().htn_gemm_tiles_scratch_bytes(rows, n, k, epilogue) if split else 0
+    scratch = torch.full(((nbytes + 15) // 16, 4), float("nan"), device=x.device) \
+        if nbytes > 0 else None
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=x.device)
+    _lib.call("htn_gemm_tiles", _lib.ptr(x), x.stride(0), _lib.ptr(w), n, k, rows, epilogue,
+              _lib.ptr(residual), residual.stride(0) if residual is not None else 0,
+              _lib.ptr(out), out.stride(0), _lib.ptr(scratch), _lib.stream(x.device))
+    return out, nbytes
+
+
+# Prompts of a few hundred rows split each tile's k range (the 8B down
+# projection at 256 and 300 rows, a 4B-wide O projection, a ragged width).
+SPLIT_CASES = [(256, 4096, 12288), (300, 2560, 4096), (260, 1000, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_CASES)
+def test_tiled_k_split_matches_oracle_and_whole_k(m, n, k):
+    from hackthenorth_amd import _lib
+    w = nrm(45, (2 * n, k), std=0.02)
+    x, res = nrm(46, (m, k)), nrm(47, (m, n))
+    wd, xd, rd = w.cuda(), x.cuda(), res.cuda()
+    top = wd[:n].contiguous()
+    out, nbytes = _tiles_abi(xd, top, n, _lib.EPI_STORE)
+    assert nbytes > 0, "this shape takes the k split"
+    within_one_ulp(out, Q.linear(x, w[:n]))
+    sums, _ = _tiles_abi(xd, top, n, _lib.EPI_STORE, split=False)
+    within_one_ulp(out, sums.cpu())
+    out, _ = _tiles_abi(xd, top, n, _lib.EPI_RESIDUAL, residual=rd)
+    torch.testing.assert_close(out.cpu().float(), Q.output_residual(x, w[:n], res).float(),
+                               atol=2e-2, rtol=2e-2)
+    # The residual epilogue rounds the sum first: split and whole may differ
+    # by one ulp of the sum plus one of the output.
+    whole, _ = _tiles_abi(xd, top, n, _lib.EPI_RESIDUAL, residual=rd, split=False)
+
+    def ulp(v):
+        return torch.pow(2.0, torch.floor(torch.log2(v.float().abs().clamp_min(1e-30))) - 7)
+    assert bool(((out.float() - whole.float()).abs() <= ulp(sums) + ulp(whole)).all())
+    # SwiGLU: one ulp of the gate or up sum is more than one of the output
+    # where the SiLU is steep; split and whole meet the general bar.
+    out, nbytes = _tiles_abi(xd, wd, n, _lib.EPI_SWIGLU)
+    gu = Q.linear(x, w)
+    torch.testing.assert_close(out.cpu().float(), Q.silu_mul(gu[:, :n], gu[:, n:]).float(),
+                               atol=2e-2, rtol=2e-2)
+    whole, _ = _tiles_abi(xd, wd, n, _lib.EPI_SWIGLU, split=False)
+    torch.testing.assert_close(out.float(), whole.float(), atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("m", [1, 3, 8, 32])
 def test_rows_match_the_batch_one_gemvs(m):
     n, k = 1024, 3072
