@@ -648,6 +648,10 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
   const int mt = row_tiles(M);
   if (p.waves > max_waves(mt)) p.waves = max_waves(mt);
   p.ks = epilogue == HTN_EPI_ARGMAX ? 1 : choose_splits(strips, p.waves, static_cast<int>(K));
+  // Residual projections of up to 32 rows keep K whole: without a split
+  // finish the next projection normalises its rows in-kernel, one launch
+  // fewer per layer (4B 5-row verify, down [2560, 9728]: 2.91 -> 2.81 ms).
+  if (epilogue == HTN_EPI_RESIDUAL && mt <= 2) p.ks = 1;
   // Plain stores of up to 32 rows (the QKV projection of verify passes and
   // batched steps) run faster on 8 waves per strip than on 16, the K split
   // left as planned (8B QKV, 5 rows: 16.9 -> 15.6 us with the rows
