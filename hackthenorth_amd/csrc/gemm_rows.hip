@@ -97,8 +97,12 @@ __device__ __forceinline__ void preload_rows(const RowsArgs& a) {
 
 constexpr int kPitch = 144;  // bytes per staged 64-element weight row (+16: conflict-free reads)
 
+// One-tile kernels that normalise their rows hold the row's first vectors
+// across the first weight issue (82-92 VGPRs unbounded: 5 waves per SIMD);
+// bounded to 8 (S = 1, 60 VGPRs) and 6 (S = 2, 80) waves per SIMD without
+// spills (8B 16-row batched step 3634 -> 3657 tok/s, 5-row verify unchanged).
 template <int MT, int S, int EPI, int W, bool NORM>
-__global__ __launch_bounds__(W * 64) void gemm_rows_kernel(RowsArgs a) {
+__global__ __launch_bounds__(W * 64, NORM && MT == 1 ? (S == 1 ? 8 : 6) : 1) void gemm_rows_kernel(RowsArgs a) {
   preload_rows(a);
   if constexpr (NORM) asm volatile("" ::"s"(a.xgain), "s"(a.xeps));
   __shared__ float red[W][MT][S][kStrip * 16];
