@@ -288,7 +288,8 @@ PREFILL_CASES = [
     (2, 16, 8, 130, 37, 300),   # batches, after a cached prefix, capacity off a tile boundary
     (1, 8, 8, 64, 1000, 1100),  # group size 1, one query tile
     (1, 40, 8, 100, 5, 128),    # group size 5
-    (1, 32, 8, 2048, 0, 2304),  # the 8B prefill: 2048 queries from slot 0
+    (1, 32, 8, 2048, 0, 2304),  # the 8B prefill: 2048 queries from slot 0 (two heads per block)
+    (2, 32, 8, 1000, 37, 1100),  # two heads per block over batches, after a cached prefix
 ]
 
 
