@@ -49,6 +49,13 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.htn_embed_gather(None, 1, null, 10, 8, null, null) == _lib.HTN_EINVAL
     assert lib.htn_attention_scratch_bytes(1, 16, 1, 575) > 0
     assert lib.htn_attention_scratch_bytes(0, 16, 1, 575) == 0
+    # The tiled GEMM's k split: partials for a short prompt's long-K
+    # projection, none for a full grid, none for k off the 64-wide steps.
+    assert lib.htn_gemm_tiles_scratch_bytes(256, 4096, 12288, _lib.EPI_RESIDUAL) > 0
+    assert lib.htn_gemm_tiles_scratch_bytes(2048, 4096, 12288, _lib.EPI_RESIDUAL) == 0
+    assert lib.htn_gemm_tiles_scratch_bytes(256, 4096, 12290, _lib.EPI_RESIDUAL) == 0
+    assert lib.htn_gemm_tiles(null, 4096, null, 16, 64, 8, 0, null, 0, null, 16, null,
+                              null) == _lib.HTN_EINVAL
     # 8-bit GEMVs reject unknown formats and missing scales.
     one = ctypes.c_void_p(256)
     assert lib.htn_gemv_w8(one, one, one, 3, one, 16, 16, null) == _lib.HTN_EINVAL
