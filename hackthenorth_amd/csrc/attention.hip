@@ -2046,20 +2046,13 @@ __global__ __launch_bounds__(HPB * kBlock) void attention_prefill(AttnArgs a) {
         }
       tmax = quad_max(tmax);
       const float m_new = fmaxf(m, tmax);
-      // Lazy rescaling: the weights stay relative to the running reference
-      // max m while no lane's max exceeds it by more than 8 (weights <= 2^8);
-      // otherwise every lane moves its reference to its new max. The ratio
-      // acc / l is the same either way.
-      if (!__all(m_new <= m + 8.f)) {
-        // A query with nothing visible yet keeps weight 0 (no inf - inf).
-        const float mr = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - mr);  // 0 while m is -inf
-        l *= alpha;
+      // A query with nothing visible yet keeps weight 0 (no inf - inf).
+      const float ms = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while m is -inf
+      l *= alpha;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] *= alpha;
-        m = m_new;
-      }
-      const float ms = m == -INFINITY ? 0.f : m;
+      for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+      m = m_new;
       uint4 phl[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
