@@ -2048,10 +2048,14 @@ __global__ __launch_bounds__(HPB * kBlock) void attention_prefill(AttnArgs a) {
       const float m_new = fmaxf(m, tmax);
       // A query with nothing visible yet keeps weight 0 (no inf - inf).
       const float ms = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while m is -inf
-      l *= alpha;
+      // Where no lane's max moved, alpha is exactly 1 (or 0 on an all-zero
+      // state) and the products are identities: the wave skips them.
+      if (!__all(m_new == m)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while m is -inf
+        l *= alpha;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+        for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+      }
       m = m_new;
       uint4 phl[4];
 #pragma unroll
