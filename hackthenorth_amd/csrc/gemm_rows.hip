@@ -659,7 +659,8 @@ Plan plan(long M, long N, long K, int epilogue, bool norm) {
   // Plain stores of up to 32 rows (the QKV projection of verify passes and
   // batched steps) run faster on 8 waves per strip than on 16, the K split
   // left as planned (8B QKV, 5 rows: 16.9 -> 15.6 us with the rows
-  // normalised in-kernel, 13.4 -> 12.4 us without; 4B within 1%).
+  // normalised in-kernel, 13.4 -> 12.4 us without; 4B within 1%); four
+  // waves were slower again (4B 5-row verify 2.80 -> 2.85 ms).
   if (epilogue == HTN_EPI_STORE && mt <= 2 && p.waves > 8) p.waves = 8;
   p.norm_bytes = norm && !norm_in_kernel(epilogue, M, K) ? align_up(M * K * 2) : 0;
   if (epilogue == HTN_EPI_ARGMAX) p.tail_bytes = static_cast<long>(strips) * M * 8;
