@@ -56,6 +56,12 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.htn_gemm_tiles_scratch_bytes(256, 4096, 12290, _lib.EPI_RESIDUAL) == 0
     assert lib.htn_gemm_tiles(null, 4096, null, 16, 64, 8, 0, null, 0, null, 16, null,
                               null) == _lib.HTN_EINVAL
+    # Checked before any launch: k off the 64-wide steps, a misaligned scratch.
+    p = ctypes.c_void_p(4096)
+    assert lib.htn_gemm_tiles(p, 128, p, 16, 100, 8, 0, null, 0, p, 16, null,
+                              null) == _lib.HTN_EUNSUPPORTED
+    assert lib.htn_gemm_tiles(p, 128, p, 16, 128, 8, 0, null, 0, p, 16, ctypes.c_void_p(4104),
+                              null) == _lib.HTN_EUNSUPPORTED
     # 8-bit GEMVs reject unknown formats and missing scales.
     one = ctypes.c_void_p(256)
     assert lib.htn_gemv_w8(one, one, one, 3, one, 16, 16, null) == _lib.HTN_EINVAL
