@@ -468,7 +468,8 @@ constexpr long kWavesPerCu = 16;
 // kernels fill the CU (eight blocks); RMSNorm kernels pay their prologue
 // once per block, so two longer-lived blocks per CU beat four (measured from
 // 3072 to 151936 row groups: e.g. the 6144-row, K = 4096 QKV projection
-// takes 9.9 us at two, 10.6 us at four); 8-bit rows are half as long, so a
+// takes 9.9 us at two, 10.6 us at four, and three, two rows per wave, made
+// the 8B step 2.831 -> 2.847 ms); 8-bit rows are half as long, so a
 // wave holds half the bytes in flight: their norm kernels keep four blocks
 // per CU (eight for 1 KB rows).
 long blocks_per_cu(long groups, bool norm, int epi, int wf, long k) {
