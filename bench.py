@@ -520,7 +520,7 @@ def cpu_baseline(model, shape_name, prompt, gpu_tokens, decode_steps=8):
     oracle = Q.Oracle(shape, weights, capacity=len(prompt) + decode_steps + 1)
     setup_s = time.perf_counter() - t0
     timer = {}
-    record = OP.teacher_forced(oracle, prompt, gpu_tokens[:decode_steps + 1], TOKEN_BAR,
+    record = OP.teacher_forced(oracle, prompt, gpu_tokens[:decode_steps + 1], OP.NEAR_TIE,
                                timer=timer)
     del oracle, weights
     cpu_name = ""

@@ -75,6 +75,7 @@ SIGNATURES = {
                                         _I64, _I64, _I, _P],
     "htn_xcc_ids": [_P, _I64, _P],
     "htn_attention_merge_in_kernel": [],
+    "htn_attention_disable_in_kernel_merge": [],
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
             "htn_gemm_tiles_scratch_bytes": _I64,

@@ -24,6 +24,9 @@
 
 #include <stdlib.h>
 
+#include <atomic>
+#include <vector>
+
 namespace htn {
 
 constexpr int D = HTN_HEAD_DIM;
@@ -2170,6 +2173,15 @@ __global__ __launch_bounds__(kBlock) void attention_merge(MergeArgs a) {
   }
 }
 
+// The XCD (hardware register XCC_ID) each block of a one-dimensional grid
+// runs on: the check of the round-robin dispatch that the XCD-affine
+// attention grid relies on.
+__global__ __launch_bounds__(kWave) void xcc_ids_kernel(int32_t* out, long n) {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  if (threadIdx.x == 0 && blockIdx.x < n) out[blockIdx.x] = static_cast<int32_t>(v & 0xfu);
+}
+
 }  // namespace htn
 
 using namespace htn;
@@ -2271,22 +2283,61 @@ void launch_partial(bool fused, const AttnArgs& a, hipStream_t st) {
   else launch_partial_t<ROWS, 1>(fused, a, st);
 }
 
-// The in-kernel merge needs every block with equal index mod 8 on one XCD:
-// true for round-robin dispatch over 1, 2, 4 or 8 XCDs. Setting
-// HTN_ATTENTION_MERGE_LAUNCH=1 keeps the separate merge launch instead.
-bool xcd_affine_merge() {
-  static int state[64];  // per device: 0 unknown, 1 on, 2 off
+// Per device: 0 unknown, 1 in-kernel merge on, 2 off.
+std::atomic<int> merge_state[64];
+
+// Launches a grid of kProbeBlocks blocks that each record their XCD and
+// checks that block i ran on the XCD of block i mod 8, the dispatch the
+// in-kernel merge relies on. Allocates and synchronises, so it runs only
+// outside stream capture, once per device.
+bool round_robin_dispatch(int dev) {
+  constexpr long kProbeBlocks = 2048;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+      !(n == 1 || n == 2 || n == 4 || n == 8))
+    return false;
+  int32_t* ids = nullptr;
+  hipStream_t s = nullptr;
+  std::vector<int32_t> host(kProbeBlocks, -1);
+  bool ok = hipMalloc(&ids, kProbeBlocks * sizeof(int32_t)) == hipSuccess &&
+            hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess;
+  if (ok) {
+    hipLaunchKernelGGL(xcc_ids_kernel, dim3(kProbeBlocks), dim3(kWave), 0, s, ids, kProbeBlocks);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(host.data(), ids, kProbeBlocks * sizeof(int32_t), hipMemcpyDeviceToHost,
+                        s) == hipSuccess &&
+         hipStreamSynchronize(s) == hipSuccess;
+  }
+  if (s) (void)hipStreamDestroy(s);
+  if (ids) (void)hipFree(ids);
+  if (!ok) return false;
+  for (long i = 0; i < kProbeBlocks; ++i)
+    if (host[i] < 0 || host[i] != host[i % 8]) return false;
+  return true;
+}
+
+// The in-kernel merge needs every block with equal index mod 8 on one XCD.
+// The first call on a device outside stream capture launches the dispatch
+// probe and keeps its answer; until then (a first call under capture) the
+// separate merge launch runs, which is correct under any dispatch. Setting
+// HTN_ATTENTION_MERGE_LAUNCH=1, or htn_attention_disable_in_kernel_merge(),
+// keeps the merge launch.
+bool xcd_affine_merge(hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  if (state[dev] == 0) {
-    int n = 0;
+  int state = merge_state[dev].load();
+  if (state == 0) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &capture) != hipSuccess ||
+        capture != hipStreamCaptureStatusNone)
+      return false;
     const char* env = getenv("HTN_ATTENTION_MERGE_LAUNCH");
-    const bool ok = !(env && env[0] == '1') &&
-                    hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
-                    (n == 1 || n == 2 || n == 4 || n == 8);
-    state[dev] = ok ? 1 : 2;
+    const bool ok = !(env && env[0] == '1') && round_robin_dispatch(dev);
+    int expected = 0;
+    merge_state[dev].compare_exchange_strong(expected, ok ? 1 : 2);
+    state = merge_state[dev].load();
   }
-  return state[dev] == 1;
+  return state == 1;
 }
 
 // The projection that reads this attention's output, for the prefetch blocks.
@@ -2424,7 +2475,7 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
   // up to four rows (one per wave) of at most 48 splits. More rows or splits
   // go to the merge launch, which spreads the rows over the GPU.
   if (a.splits > 1 && a.splits <= 48 && rows <= 4 && !a.stream && heads <= kMaxCounterPairs &&
-      out_pairs && xcd_affine_merge())
+      out_pairs && xcd_affine_merge(st))
     a.done = reinterpret_cast<unsigned*>(sbase);
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
   // Prefetch of the next projection's weights: only with the XCD-affine grid
@@ -2591,19 +2642,6 @@ extern "C" int htn_prologue_attention_prefetch(
                             out, B, Hkv, groups, scratch, &next, stream);
 }
 
-namespace htn {
-
-// Diagnostic: the XCD (hardware register XCC_ID) each block of a one-
-// dimensional grid runs on, for checking the round-robin dispatch that the
-// XCD-affine attention grid relies on.
-__global__ __launch_bounds__(kWave) void xcc_ids_kernel(int32_t* out, long n) {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  if (threadIdx.x == 0 && blockIdx.x < n) out[blockIdx.x] = static_cast<int32_t>(v & 0xfu);
-}
-
-}  // namespace htn
-
 extern "C" int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream) {
   if (!out || blocks <= 0 || blocks > (1L << 20)) return HTN_EINVAL;
   hipLaunchKernelGGL(xcc_ids_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
@@ -2611,4 +2649,11 @@ extern "C" int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream) {
   return launch_status();
 }
 
-extern "C" int htn_attention_merge_in_kernel() { return xcd_affine_merge() ? 1 : 0; }
+extern "C" int htn_attention_merge_in_kernel() { return xcd_affine_merge(nullptr) ? 1 : 0; }
+
+extern "C" int htn_attention_disable_in_kernel_merge() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HTN_EINVAL;
+  merge_state[dev].store(2);
+  return HTN_OK;
+}

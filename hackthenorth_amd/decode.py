@@ -16,7 +16,8 @@ advances the position.
 import torch
 
 from ._lib import HEAD_DIM
-from .kernels.attention import decode_attention, grouped_attention, prologue_attention
+from .kernels.attention import (check_xcd_merge, decode_attention, grouped_attention,
+                                prologue_attention)
 from .kernels.down import down_residual
 from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
@@ -300,6 +301,11 @@ class DecodeState:
     def step(self, model):
         forward(model, self.token, self.cache, self.position, rotary=self.rotary,
                 out=self.token, advance=self.position)
+
+    def check_merge(self):
+        """Raise if an in-kernel attention merge of this device saw a split on
+        another XCD (kernels.attention.check_xcd_merge); synchronises."""
+        check_xcd_merge(self.model.device)
 
     def capture(self, model):
         self.cache.prefill = False

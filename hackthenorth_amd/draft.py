@@ -19,6 +19,7 @@ consumed dk, so the next cycle first steps it on dk.
 import torch
 
 from .decode import DecodeState
+from .kernels.attention import check_xcd_merge
 from .prefill import prefill
 from .speculate import verified_tokens
 
@@ -110,14 +111,25 @@ class DraftSpeculator:
             yield [current]
             yield from self.continue_from(current, len(prompt), max_new_tokens - 1)
 
+    def _check_merge(self):
+        check_xcd_merge(self.target.device)
+        if self.draft.device != self.target.device:
+            check_xcd_merge(self.draft.device)
+
     def continue_from(self, current, position, count):
         """Yield `count` more tokens after `current`, which sits at `position`
-        (both caches hold every earlier position)."""
+        (both caches hold every earlier position). The in-kernel attention
+        merge's mismatch count is read after the first cycle and before the
+        last tokens are yielded (kernels.attention.check_xcd_merge)."""
         with torch.inference_mode():
             emitted_count = 0
             catch_up = None
+            cycles = 0
             while emitted_count < count:
                 emitted, proposal = self.cycle(current, position, catch_up)
+                cycles += 1
+                if cycles == 1 or emitted_count + len(emitted) >= count:
+                    self._check_merge()
                 all_accepted = len(emitted) == self.k + 1
                 catch_up = proposal[-1] if all_accepted else None
                 position += len(emitted)

@@ -8,6 +8,7 @@ import torch
 
 from .decode import DecodeState, stream_decode
 from .draft import DraftSpeculator
+from .kernels.attention import XcdMergeError, check_xcd_merge
 from .model import Qwen3Model
 from .prefill import prefill
 from .speculate import BackoffPromptLookup
@@ -34,8 +35,29 @@ class Engine:
         self.speculator = None
 
     def generate(self, input_ids: list, max_new_tokens: int):
+        """Yield max_new_tokens lists of one greedy token per sequence.
+
+        The in-kernel attention merge assumes round-robin workgroup dispatch
+        (checked when the library first runs on a device); every request
+        also reads the merges' mismatch count after its second output and
+        before its last (check_xcd_merge), and raises XcdMergeError, with the
+        captured states dropped and the merge launch switched on, if a merge
+        saw a split from another XCD.
+        """
         if max_new_tokens <= 0:
             return
+        device = self.model.device
+        try:
+            for i, tokens in enumerate(self._generate(input_ids, max_new_tokens)):
+                if i == 1 or i == max_new_tokens - 1:
+                    check_xcd_merge(device)
+                yield tokens
+        except XcdMergeError:
+            self.state = None
+            self.speculator = None
+            raise
+
+    def _generate(self, input_ids, max_new_tokens):
         if self.draft is not None and self.speculative and len(input_ids) == 1:
             shape = (1, len(input_ids[0]), max_new_tokens)
             if self.speculator is None or self.speculator.shape != shape:

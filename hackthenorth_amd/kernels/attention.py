@@ -57,6 +57,30 @@ def xcd_merge_mismatches(device=None, reset=False):
     return total
 
 
+class XcdMergeError(RuntimeError):
+    """An in-kernel split merge found a split of its pair on another XCD."""
+
+
+def check_xcd_merge(device=None):
+    """Raise XcdMergeError if any in-kernel split merge on `device` has found a
+    split of its (batch, kv head) pair on another XCD since the last check.
+
+    Before raising, the device is switched to the separate merge launch, so
+    states built afterwards are correct; graphs captured before keep the
+    in-kernel merge and must be captured again. Reads device memory (one
+    small copy per attention scratch buffer), so it synchronises.
+    """
+    count = xcd_merge_mismatches(device, reset=True)
+    if count:
+        index = torch.device(device).index if device is not None else None
+        with torch.cuda.device(index if index is not None else torch.cuda.current_device()):
+            _lib.call("htn_attention_disable_in_kernel_merge")
+        raise XcdMergeError(
+            f"{count} in-kernel attention merges saw splits from another XCD: workgroup "
+            "dispatch is not round-robin on this device; the in-kernel merge is now off "
+            "(separate merge launch), and states captured before must be rebuilt")
+
+
 def _check_cache(keys, values, batch, kv_heads):
     if keys.shape != values.shape or keys.dim() != 4 or keys.shape[0] != batch \
             or keys.shape[1] != kv_heads or keys.shape[3] != _lib.HEAD_DIM \

@@ -385,14 +385,23 @@ int htn_prologue_attention_prefetch(
     void* scratch, const void* next_w, int64_t next_n, int64_t next_k, int next_format,
     htn_stream_t stream);
 
-/* Diagnostics of the in-kernel attention merge; no counterpart in the
- * reference. htn_xcc_ids writes, for each block b < blocks of a
+/* Diagnostics and control of the in-kernel attention merge; no counterpart
+ * in the reference. htn_xcc_ids writes, for each block b < blocks of a
  * one-dimensional grid, the XCD it ran on (hardware register XCC_ID), so a
  * test can confirm the round-robin dispatch the merge relies on (blocks with
- * equal index mod 8 share an XCD). htn_attention_merge_in_kernel returns 1 if
- * the attention entry points merge splits in-kernel on the current device. */
+ * equal index mod 8 share an XCD). The first attention call on a device
+ * outside stream capture runs that check itself (a 2048-block grid, one
+ * small allocation, synchronous) and merges in-kernel only if it holds.
+ * htn_attention_merge_in_kernel returns 1 if the attention entry points merge
+ * splits in-kernel on the current device (running the check if it has not
+ * run). htn_attention_disable_in_kernel_merge switches the current device to
+ * the separate merge launch for the rest of the process (launches captured
+ * earlier keep the mode they were captured with); the host calls it when a
+ * merge has counted a split from another XCD (the 32-bit word at byte
+ * HTN_ATTENTION_XCD_MISMATCH_BYTE of the attention scratch). */
 int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream);
 int htn_attention_merge_in_kernel(void);
+int htn_attention_disable_in_kernel_merge(void);
 
 #ifdef __cplusplus
 }

@@ -160,11 +160,13 @@ def generate_weights(shape, seed=0, std=0.02, weight_format="bf16"):
 
 # ---------------------------------------------------------------- per-op math
 
-def rms_norm(x, gain, eps):
-    """dryft/engine/kernels/rmsnorm.py:64-81."""
-    v = x.float()
+def rms_norm(x, gain, eps, acc=torch.float32):
+    """dryft/engine/kernels/rmsnorm.py:64-81. `acc` is the arithmetic type
+    between the bf16 roundings (float32 as the reference; float64 gives a
+    second, independently rounded evaluation of the same formula)."""
+    v = x.to(acc)
     inv = torch.rsqrt(v.square().mean(-1, keepdim=True) + eps)
-    return (gain.float() * (v * inv).to(BF16).float()).to(BF16)
+    return (gain.to(acc) * (v * inv).to(BF16).to(acc)).to(BF16)
 
 
 def add_rms_norm(x, residual, gain, eps):
@@ -183,11 +185,11 @@ def linear_w8(x, values, scale):
     return ((x.float() @ values.float().T) * scale.float()).to(BF16)
 
 
-def silu_mul(gate, up):
+def silu_mul(gate, up, acc=torch.float32):
     """dryft/engine/kernels/fused.py:160-168 and projection.py:26-32."""
-    g = gate.float()
+    g = gate.to(acc)
     act = (g * torch.sigmoid(g)).to(BF16)
-    return (act.float() * up.float()).to(BF16)
+    return (act.to(acc) * up.to(acc)).to(BF16)
 
 
 def output_residual(x, weight, residual):
@@ -205,20 +207,20 @@ def rope_tables(capacity, head_dim, theta):
     return emb.cos().to(BF16), emb.sin().to(BF16)
 
 
-def norm_rope(x, gain, cos, sin, eps):
+def norm_rope(x, gain, cos, sin, eps, acc=torch.float32):
     """Per-head RMSNorm then RoPE with rotate_half (kernels/fused.py:17-30).
 
     x [..., T, H, D]; cos/sin broadcastable to [..., T, 1, D].
     """
-    n = rms_norm(x, gain, eps).float()
+    n = rms_norm(x, gain, eps, acc).to(acc)
     half = x.shape[-1] // 2
     rot = torch.cat((-n[..., half:], n[..., :half]), dim=-1)
-    left = (n * cos.float()).to(BF16).float()
-    right = (rot * sin.float()).to(BF16).float()
+    left = (n * cos.to(acc)).to(BF16).to(acc)
+    right = (rot * sin.to(acc)).to(BF16).to(acc)
     return (left + right).to(BF16)
 
 
-def attention(q, keys, values, positions):
+def attention(q, keys, values, positions, acc=torch.float32):
     """GQA over a fixed-capacity cache (kernels/attention.py:13-63 semantics).
 
     q [B, Hq, Q, D] bf16; keys/values [B, Hkv, cap, D]; positions [Q] absolute.
@@ -228,9 +230,9 @@ def attention(q, keys, values, positions):
     groups = q.shape[1] // keys.shape[1]
     # Slots after the last query position are never touched (they may hold NaN).
     last = int(positions.max()) + 1
-    k = keys[:, :, :last].float().repeat_interleave(groups, dim=1)
-    v = values[:, :, :last].float().repeat_interleave(groups, dim=1)
-    scores = (q.float() @ k.transpose(-1, -2)) * (d ** -0.5)
+    k = keys[:, :, :last].to(acc).repeat_interleave(groups, dim=1)
+    v = values[:, :, :last].to(acc).repeat_interleave(groups, dim=1)
+    scores = (q.to(acc) @ k.transpose(-1, -2)) * (d ** -0.5)
     visible = torch.arange(last)[None, :] <= positions[:, None]
     scores = scores.masked_fill(~visible[None, None], float("-inf"))
     p = torch.softmax(scores, dim=-1)
@@ -257,24 +259,40 @@ def new_cache(shape, capacity, batch=1, fill=0.0):
 
 @dataclass
 class Oracle:
+    """The reference's forward over `weights`.
+
+    `acc` is the arithmetic type between the bf16 rounding boundaries:
+    float32, as the reference computes, or float64, which evaluates the same
+    formula with every product and sum rounded differently (the roundings to
+    bf16 stay where they are). The two give two legitimate evaluation orders
+    of one model; where they pick different greedy tokens, the choice is
+    within the formula's own rounding noise.
+    """
     shape: Shape
     weights: dict
     capacity: int
+    acc: torch.dtype = torch.float32
     cos: torch.Tensor = field(init=False)
     sin: torch.Tensor = field(init=False)
     f32: dict = field(init=False)
 
     def __post_init__(self):
         s = self.shape
+        if self.acc not in (torch.float32, torch.float64):
+            raise ValueError("acc must be torch.float32 or torch.float64")
         self.cos, self.sin = rope_tables(self.capacity, s.head_dim, s.theta)
         # fp32 copies of the bf16 weights: products of bf16 are exact in fp32.
-        self.f32 = {k: v.float() for k, v in self.weights.items() if v.dim() == 2}
+        # The float64 evaluation converts each weight when it is used instead
+        # (a resident copy would take four times the bf16 bytes).
+        self.f32 = ({k: v.float() for k, v in self.weights.items() if v.dim() == 2}
+                    if self.acc == torch.float32 else {})
 
     def _dot(self, x, name):
-        """fp32 dot products, times the row scales of an 8-bit weight."""
-        y = x.float() @ self.f32[name].T
+        """Dot products in `acc`, times the row scales of an 8-bit weight."""
+        w = self.f32[name] if self.acc == torch.float32 else self.weights[name].to(self.acc)
+        y = x.to(self.acc) @ w.T
         scale = self.weights.get(name + ".scale")
-        return y if scale is None else y * scale
+        return y if scale is None else y * scale.to(self.acc)
 
     def _linear(self, x, name):
         return self._dot(x, name).to(BF16)
@@ -289,29 +307,31 @@ class Oracle:
         w = self.weights
         b, t = h.shape[:2]
         d = s.head_dim
+        acc = self.acc
         cos = self.cos[positions][None, :, None, :]      # [1, T, 1, D]
         sin = self.sin[positions][None, :, None, :]
-        n = rms_norm(h, w[f"{l}.ln1"], s.eps)
+        n = rms_norm(h, w[f"{l}.ln1"], s.eps, acc)
         qkv = self._linear(n, f"{l}.qkv")
         q, k, v = qkv.split((s.q_heads * d, s.kv_heads * d, s.kv_heads * d), -1)
-        q = norm_rope(q.view(b, t, s.q_heads, d), w[f"{l}.q_norm"], cos, sin, s.eps)
-        k = norm_rope(k.view(b, t, s.kv_heads, d), w[f"{l}.k_norm"], cos, sin, s.eps)
+        q = norm_rope(q.view(b, t, s.q_heads, d), w[f"{l}.q_norm"], cos, sin, s.eps, acc)
+        k = norm_rope(k.view(b, t, s.kv_heads, d), w[f"{l}.k_norm"], cos, sin, s.eps, acc)
         v = v.reshape(b, t, s.kv_heads, d)
         cache.keys[l][:, :, positions] = k.transpose(1, 2)
         cache.values[l][:, :, positions] = v.transpose(1, 2)
-        a = attention(q.transpose(1, 2), cache.keys[l], cache.values[l], positions)
+        a = attention(q.transpose(1, 2), cache.keys[l], cache.values[l], positions, acc)
         a = a.transpose(1, 2).reshape(b, t, s.q_heads * d)
-        r = (self._linear(a, f"{l}.o").float() + h.float()).to(BF16)
-        m = rms_norm(r, w[f"{l}.ln2"], s.eps)
+        r = (self._linear(a, f"{l}.o").to(acc) + h.to(acc)).to(BF16)
+        m = rms_norm(r, w[f"{l}.ln2"], s.eps, acc)
         gu = self._linear(m, f"{l}.gate_up")
-        act = silu_mul(gu[..., :s.ffn], gu[..., s.ffn:])
-        return (self._linear(act, f"{l}.down").float() + r.float()).to(BF16)
+        act = silu_mul(gu[..., :s.ffn], gu[..., s.ffn:], acc)
+        return (self._linear(act, f"{l}.down").to(acc) + r.to(acc)).to(BF16)
 
-    def forward(self, ids, cache, positions, last_only=True, record=None):
+    def forward(self, ids, cache, positions, last_only=True, record=None, keep=None):
         """ids [B, T] int64, positions [T] absolute; returns (tokens, logits_f32, logits_bf16).
 
         Writes K/V of the new tokens into cache slots `positions` (decode.py:35-46).
         `record`, when a list, receives the bf16 hidden state after every layer.
+        `keep` (with last_only=False) limits the head to the last `keep` rows.
         """
         s = self.shape
         w = self.weights
@@ -320,10 +340,11 @@ class Oracle:
             h = self.layer(l, h, cache, positions)
             if record is not None:
                 record.append(h.clone())
-        x = rms_norm(h[:, -1:] if last_only else h, w["norm"], s.eps)
+        rows = h[:, -1:] if last_only else (h[:, -keep:] if keep else h)
+        x = rms_norm(rows, w["norm"], s.eps, self.acc)
         logits = self._dot(x, "lm_head")
         logits_bf16 = logits.to(BF16)
-        return greedy(logits_bf16), logits, logits_bf16
+        return greedy(logits_bf16), logits.float(), logits_bf16
 
     def greedy_decode(self, prompt, steps, record_steps=0):
         """Prefill the prompt, then `steps` greedy tokens (first from the prefill).
@@ -355,8 +376,24 @@ class Oracle:
         seq = list(prompt) + list(generated[:-1])
         ids = torch.tensor([seq], dtype=torch.int64)
         cache = new_cache(self.shape, max(self.capacity, len(seq)))
-        _, lf, _ = self.forward(ids, cache, torch.arange(len(seq)), last_only=False)
-        return lf[0, len(prompt) - 1:]
+        _, lf, _ = self.forward(ids, cache, torch.arange(len(seq)), last_only=False,
+                                keep=len(generated))
+        return lf[0]
+
+    def stepwise_logits(self, prompt, generated):
+        """The same logits as teacher_forced_logits in another evaluation order:
+        one causal pass over the prompt, then each generated token fed alone
+        against the cache (the decode loop's order, decode.py:126-138)."""
+        ids = torch.as_tensor(prompt, dtype=torch.int64).view(1, -1)
+        p = ids.shape[1]
+        cache = new_cache(self.shape, max(self.capacity, p + len(generated)))
+        _, lf, _ = self.forward(ids, cache, torch.arange(p))
+        out = [lf[0, 0]]
+        for i in range(1, len(generated)):
+            _, lf, _ = self.forward(torch.tensor([[int(generated[i - 1])]]), cache,
+                                    torch.tensor([p + i - 1]))
+            out.append(lf[0, 0])
+        return torch.stack(out)
 
 
 def prompt_ids(count, vocab, seed=1, stream=7):

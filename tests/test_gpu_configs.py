@@ -19,14 +19,15 @@ weights. Caches at long contexts hold N(0,1) values in the slots before the
 query (the kernels' cost and numerics do not depend on how they were written);
 the oracle gets a copy of the same cache.
 
-Bars: per layer cosine >= 0.9999 and max-abs error 2e-2 of the layer's full
-scale (check_hidden says why the scale); appended cache rows within one bf16
-ulp; greedy ids equal to the oracle's pick unless the oracle's fp32 logit
-deficit of the emitted token is below TOKEN_BAR or its bf16 margin below
-TOKEN_BAR / 2 (oracle/parity.py); each test prints identical/total, the largest
-deficit and the largest bf16 margin (the smallest per-logit perturbation that
-makes the emitted token the bf16 greedy pick). The LM-head test holds the
-north star's 1e-3 on the margin: one GEMV's logits carry no accumulated noise.
+Bars: per layer, every element within HIDDEN_ULPS bf16 ulps of max(|expected|,
+the layer's rms) and cosine >= 0.9999 (parity_helpers.check_hidden); appended
+cache rows within one bf16 ulp; greedy ids equal to the oracle's pick, or a
+near-tie within the north star's 1e-3, or a step where the oracle's own
+evaluation orders (token-by-token instead of one causal pass, float64 instead
+of float32 between the same bf16 roundings) disagree at least as much
+(oracle/parity.py); each test prints the classification of every differing
+step. The LM-head test admits near-ties only: one GEMV's logits carry no
+accumulated noise.
 """
 import dataclasses
 import json
@@ -38,6 +39,7 @@ import torch
 from oracle import parity as OP
 from oracle import qwen3 as Q
 from oracle import rng as ORNG
+from parity_helpers import check_hidden, check_record, record_sequence
 from hackthenorth_amd import decode as D
 from hackthenorth_amd.draft import DraftSpeculator
 from hackthenorth_amd.engine import Engine
@@ -49,26 +51,8 @@ from hackthenorth_amd.model import (STREAM_LM_HEAD, STREAM_LM_HEAD_SCALE, Qwen3M
 from hackthenorth_amd.quant import QuantizedWeight
 
 pytestmark = pytest.mark.gpu
-TOKEN_BAR = 2e-2
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 NAMES = {"tiny": "tiny", "0.6b": "qwen3-0.6b", "4b": "qwen3-4b", "8b": "qwen3-8b"}
-
-
-def check_hidden(label, actual, expected):
-    """Per-layer bar: cosine >= 0.9999 and max-abs error <= 2e-2 of the
-    layer's full scale (max |expected|, at least 1). At these shapes layer
-    outputs reach |h| of 8-16 in bf16 (one ulp = 0.0625) and, with 8-bit
-    weights and scales U(0.001, 0.01), 1e4-1e5 (one ulp = 512), so a literal
-    2e-2 would demand bit-identical fp32 summation orders."""
-    act = actual.detach().cpu().float().reshape(-1)
-    exp = expected.detach().cpu().float().reshape(-1)
-    err = float((act - exp).abs().max())
-    scale = max(1.0, float(exp.abs().max()))
-    cos = float(torch.nn.functional.cosine_similarity(act.double(), exp.double(), dim=0))
-    print(f"{label}: max_abs_err={err:.4g} full_scale={scale:.4g} "
-          f"normalised_err={err / scale:.3g} cos={cos:.7f}", flush=True)
-    assert err <= 2e-2 * scale
-    assert cos >= 0.9999
 
 
 def within_one_ulp(label, actual, expected):
@@ -90,13 +74,6 @@ def synthetic_cache(model, capacity, filled, seed_stream):
 
 def oracle_cache(cache):
     return Q.Cache(cache.storage[:, 0].cpu().clone(), cache.storage[:, 1].cpu().clone())
-
-
-def check_record(record, label):
-    print(record.line(label), flush=True)
-    summary = record.summary()
-    assert summary["over_bar"] == 0, summary
-    return summary
 
 
 @pytest.mark.parametrize("fmt,ctx", [("bf16", 2048), ("int8", 8192), ("fp8_e4m3", 8192)])
@@ -141,7 +118,8 @@ def test_8b_lm_head_argmax_matches_oracle(fmt):
         wf = torch.from_numpy(ORNG.w8_values(codes, fmt)).view(vocab, hidden)
         scale = w.scale.cpu()
     gain = DR.normal_(torch.empty((hidden,), dtype=torch.bfloat16, device=dev), 4, 9, 1.0)
-    record = OP.TokenRecord(1e-3)
+    record = OP.TokenRecord()
+    normed = []
     with torch.inference_mode():
         for row in range(6):
             x = DR.normal_(torch.empty((hidden,), dtype=torch.bfloat16, device=dev), 30 + row,
@@ -149,12 +127,19 @@ def test_8b_lm_head_argmax_matches_oracle(fmt):
             token = torch.empty((1,), dtype=torch.int64, device=dev)
             greedy_head(x, gain, 1e-6, w, token)
             xn = Q.rms_norm(x.cpu(), gain.cpu(), 1e-6)
+            normed.append(xn)
             logits = xn.float() @ wf.T
             if scale is not None:
                 logits = logits * scale
             record.add(row, logits, int(token))
-    summary = check_record(record, f"8b LM head {fmt}")
-    assert summary["margin_over_1e-3"] == 0
+
+    def float64(step):
+        logits = normed[step].double() @ wf.double().T
+        return logits if scale is None else logits * scale.double()
+
+    summary = check_record(record, f"8b LM head {fmt}", {"float64": float64})
+    # One GEMV: a differing id must be a near-tie, not accumulated noise.
+    assert summary["oracle_noise"] == 0, summary
 
 
 def test_4b_verify_rows_at_context_4096_match_oracle():
@@ -172,15 +157,40 @@ def test_4b_verify_rows_at_context_4096_match_oracle():
         record = []
         got = D.forward(model, torch.tensor([ids], device="cuda"), cache, positions,
                         last_only=False, rotary=rotary, record=record)[0].cpu()
-        orec = []
+        clean = oracle_cache(cache)
         _, logits, _ = oracle.forward(torch.tensor([ids]), ocache, torch.arange(ctx, ctx + rows),
-                                      last_only=False, record=orec)
+                                      last_only=False)
+        # Per layer on identical inputs: the oracle's layer l gets the HIP
+        # rows that entered the HIP's layer l, and a cache holding the same
+        # earlier slots.
+        per_layer = Q.Cache(clean.keys.clone(), clean.values.clone())
+        h = oracle.weights["embed"][torch.tensor([ids])]
+        opos = torch.arange(ctx, ctx + rows)
         for layer in range(layers):
-            check_hidden(f"4b verify rows ctx {ctx} layer {layer}", record[layer], orec[layer])
-        tokens = OP.TokenRecord(TOKEN_BAR)
+            expected = oracle.layer(layer, h, per_layer, opos)
+            check_hidden(f"4b verify rows ctx {ctx} layer {layer}", record[layer], expected)
+            for kv, name in ((0, "k"), (1, "v")):
+                mine = cache.storage[layer, kv, 0, :, ctx:ctx + rows]
+                ref = (per_layer.keys if kv == 0 else per_layer.values)[layer][0, :, ctx:ctx + rows]
+                check_hidden(f"4b verify rows layer {layer} new {name} rows", mine, ref)
+            h = record[layer].cpu()
+        tokens = OP.TokenRecord()
         for i, t in enumerate(got.tolist()):
             tokens.add(i, logits[0, i], t)
-        check_record(tokens, "4b 5-row verify")
+
+        def stepwise():
+            c = Q.Cache(clean.keys.clone(), clean.values.clone())
+            return torch.stack([oracle.forward(torch.tensor([[t]]), c, torch.tensor([ctx + i]))[1]
+                                [0, 0] for i, t in enumerate(ids)])
+
+        def float64():
+            o64 = Q.Oracle(oshape, oracle.weights, ctx + rows, acc=torch.float64)
+            c = Q.Cache(clean.keys.clone(), clean.values.clone())
+            return o64.forward(torch.tensor([ids]), c, torch.arange(ctx, ctx + rows),
+                               last_only=False)[1][0]
+
+        check_record(tokens, "4b 5-row verify",
+                     OP.Orders(stepwise=stepwise, float64=float64).callables())
         # The captured verify graph gives the eager pass's bits.
         state = D.DecodeState(model, 1, ctx, 4, speculative=True, draft_tokens=rows - 1)
         state.cache.storage[..., :ctx, :].copy_(cache.storage[..., :ctx, :])
@@ -205,18 +215,16 @@ def test_0p6b_decode_at_context_512_teacher_forced():
     # splits on its own XCD.
     assert A.xcd_merge_mismatches() == 0
     oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), prompt_len + steps)
-    logits = oracle.teacher_forced_logits(prompt, emitted)
-    record = OP.TokenRecord(TOKEN_BAR)
-    for i, t in enumerate(emitted):
-        record.add(i, logits[i], t)
-    check_record(record, "0.6b ctx 512, 64 steps")
+    record_sequence(oracle, prompt, emitted, "0.6b ctx 512, 64 steps")
 
 
 def test_8b_prefill_2048_matches_oracle_batched_forward():
     """The captured batched prefill of a 2048-token prompt (two 8B layers):
-    every prompt slot's K/V against the oracle's batched forward, the first
-    token against its logits, and a replay on a second prompt equal to the
-    eager pass on that prompt."""
+    per layer on identical inputs, every prompt slot's K/V and every row of
+    the layer output against the oracle's batched layer; the first token
+    against the oracle's whole forward; the graph's caches and token equal
+    to the eager pass's; a replay on a second prompt equal to the eager pass
+    on that prompt."""
     layers, length = 2, 2048
     oshape = dataclasses.replace(Q.SHAPES["8b"], layers=layers, vocab=64)
     cfg = shape_config("qwen3-8b", num_hidden_layers=layers, vocab_size=64)
@@ -227,16 +235,34 @@ def test_8b_prefill_2048_matches_oracle_batched_forward():
         state = D.DecodeState(model, 1, length, 2)
         first = prefill(model, state, torch.tensor([prompts[0]], device="cuda"))
         assert int(state.position) == length
+        # The same pass eagerly, with every layer's output rows recorded.
+        cache = D.KVCache(model, 1, length + 1)
+        rows = []
+        eager_first = D.forward(model, torch.tensor([prompts[0]], device="cuda"), cache,
+                                torch.arange(length, device="cuda"), rotary=state.rotary,
+                                record=rows)
+        assert torch.equal(eager_first, first)
+        assert torch.equal(cache.storage[..., :length, :], state.cache.storage[..., :length, :])
         ocache = Q.new_cache(oshape, length + 1)
-        _, logits, _ = oracle.forward(torch.tensor([prompts[0]]), ocache, torch.arange(length))
+        positions = torch.arange(length)
+        h = oracle.weights["embed"][torch.tensor([prompts[0]])]
         for layer in range(layers):
+            expected = oracle.layer(layer, h, ocache, positions)
+            check_hidden(f"prefill 2048 layer {layer} output rows", rows[layer], expected)
             for kv, name in ((0, "k"), (1, "v")):
                 mine = state.cache.storage[layer, kv, 0, :, :length]
                 ref = (ocache.keys if kv == 0 else ocache.values)[layer][0, :, :length]
                 check_hidden(f"prefill 2048 layer {layer} {name} cache", mine, ref)
-        record = OP.TokenRecord(TOKEN_BAR)
+            h = rows[layer].cpu()
+        _, logits, _ = oracle.forward(torch.tensor([prompts[0]]), Q.new_cache(oshape, length + 1),
+                                      positions)
+        record = OP.TokenRecord()
         record.add(0, logits[0, 0], int(first[0, 0]))
-        check_record(record, "8b prefill 2048 first token")
+        o64 = Q.Oracle(oshape, oracle.weights, length + 1, acc=torch.float64)
+        check_record(record, "8b prefill 2048 first token", {
+            "float64": lambda step: o64.forward(torch.tensor([prompts[0]]),
+                                                Q.new_cache(oshape, length + 1),
+                                                torch.arange(length))[1][0, 0]})
         replayed = int(prefill(model, state, torch.tensor([prompts[1]], device="cuda"))[0, 0])
         kv_replay = state.cache.storage[..., :length, :].clone()
         eager = int(state.prefill(model, torch.tensor([prompts[1]], device="cuda"))[0, 0])
@@ -262,20 +288,10 @@ def test_draft_speculation_emits_oracle_greedy_ids(draft_seed, k):
     got = [t[0] for t in spec.generate(prompt, steps)]
     shape = Q.SHAPES["tiny"]
     oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), len(prompt) + steps)
-    logits = oracle.teacher_forced_logits(prompt, got)
-    record = OP.TokenRecord(TOKEN_BAR)
-    for i, t in enumerate(got):
-        record.add(i, logits[i], t)
-    check_record(record, f"tiny draft seed {draft_seed} k {k} (acceptance "
-                         f"{spec.acceptance:.2f})")
+    record_sequence(oracle, prompt, got, f"tiny draft seed {draft_seed} k {k} (acceptance "
+                                         f"{spec.acceptance:.2f})")
     same = sum(a == b for a, b in zip(got, meta["tokens"]))
     print(f"{same}/{steps} ids equal to the oracle's free-running greedy decode", flush=True)
-    # Free-running sequences may part only at a step where the oracle's own
-    # top-2 gap is below the bar.
-    for i, (a, e) in enumerate(zip(got, meta["tokens"])):
-        if a != e:
-            assert meta["top2_gap_fp32"][i] < TOKEN_BAR, (i, a, e)
-            break
 
 
 @pytest.mark.parametrize("shape_name,batch,prompt_len,steps",
@@ -288,10 +304,6 @@ def test_engine_generate_batched_teacher_forced(tmp_path, shape_name, batch, pro
     outs = list(engine.generate(prompts, steps))
     assert len(outs) == steps and all(len(o) == batch for o in outs)
     oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), prompt_len + steps)
-    record = OP.TokenRecord(TOKEN_BAR)
     for b in range(batch):
-        seq = [o[b] for o in outs]
-        logits = oracle.teacher_forced_logits(prompts[b], seq)
-        for i, t in enumerate(seq):
-            record.add(b * steps + i, logits[i], t)
-    check_record(record, f"{shape_name} batch {batch}, {steps} steps")
+        record_sequence(oracle, prompts[b], [o[b] for o in outs],
+                        f"{shape_name} batch {batch}, sequence {b}, {steps} steps")

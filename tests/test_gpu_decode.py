@@ -3,17 +3,15 @@ fixtures written by the CPU oracle (tests/golden/make_golden.py).
 
 Bars:
   * per layer, on identical inputs: bf16 outputs within max-abs 2e-2 (+ 2e-2
-    relative) and cosine >= 0.9999 of the oracle's (the north star's bar);
+    relative) and cosine >= 0.9999 of the oracle's (the north star's bar),
+    and every element within HIDDEN_ULPS bf16 ulps of max(|expected|, the
+    layer's rms);
   * the free-running states keep cosine >= 0.9999 at every layer;
-  * greedy ids: teacher-forced along the oracle's own 64-token greedy
-    sequence, every HIP prediction equals the oracle's argmax unless the
-    oracle's logit deficit of the HIP token is below DEFICIT (the reference
-    judge's rule, dryft/agent/benchmark_gpu.py:132-157, which allows 2.0);
-    the free-running decode may diverge only at such a step.
-DEFICIT is 2e-2, not the north star's 1e-3: per-layer differences of one bf16
-ulp (fp32 summation order, expf) compound over 28 layers to hidden states at
-cosine ~0.9999, i.e. logit noise of ~1e-2, so two independent fp32
-accumulations of this model disagree at top-2 gaps of that size.
+  * greedy ids, teacher-forced along the emitted (or the oracle's own)
+    sequence: each equal to the oracle's pick, or a near-tie within the north
+    star's 1e-3, or at a step where the oracle's own evaluation orders
+    (token-by-token decode, float64 between the same bf16 roundings) disagree
+    at least as much (oracle/parity.py); none unexplained.
 """
 import json
 import os
@@ -22,7 +20,9 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import parity as OP
 from oracle import qwen3 as Q
+from parity_helpers import check_hidden, check_record, record_sequence
 from hackthenorth_amd import decode as D
 from hackthenorth_amd.kernels.embed import embed_gather
 from hackthenorth_amd.engine import Engine
@@ -43,19 +43,23 @@ def load(name):
     return meta, hidden
 
 
-DEFICIT = 2e-2
+def oracle_for(meta, extra=0):
+    shape = Q.SHAPES[meta["shape"]]
+    return Q.Oracle(shape, Q.generate_weights(shape, seed=meta["seed"]),
+                    meta["capacity"] + extra)
 
 
-def check_tokens(actual, meta):
-    """Free-running ids: equal to the oracle's until a divergence at a step
-    whose oracle top-2 gap is below DEFICIT; returns that step or None."""
-    expected, gaps = meta["tokens"], meta["top2_gap_fp32"]
-    for i, (a, e) in enumerate(zip(actual, expected)):
+def check_tokens(actual, meta, label):
+    """Free-running ids: every emitted token checked teacher-forced along the
+    emitted sequence itself; returns the first step that parts from the
+    golden (the oracle's own free-running decode), or None."""
+    record_sequence(oracle_for(meta), meta["prompt"], actual, label)
+    for i, (a, e) in enumerate(zip(actual, meta["tokens"])):
         if a != e:
-            assert gaps[i] < DEFICIT, f"step {i}: got {a}, oracle {e}, oracle top-2 gap {gaps[i]}"
-            print(f"free-running divergence at step {i} (oracle top-2 gap {gaps[i]:.4g})")
+            print(f"{label}: parts from the golden ids at step {i} "
+                  f"(oracle top-2 gap there {meta['top2_gap_fp32'][i]:.4g})", flush=True)
             return i
-    assert len(actual) == len(expected)
+    assert len(actual) == len(meta["tokens"])
     return None
 
 
@@ -118,7 +122,7 @@ def test_each_layer_matches_oracle_on_identical_inputs(name):
             print(f"{name} layer {layer}: max_abs_err={float(err.max()):.4g} cos={cos:.7f} "
                   f"max|h|={float(exp.abs().max()):.3g}", flush=True)
             torch.testing.assert_close(act, exp, atol=2e-2, rtol=2e-2)
-            assert cos >= 0.9999
+            check_hidden(f"{name} layer {layer}", mine, expected)
             h = mine
 
 
@@ -158,24 +162,27 @@ def test_graph_decode_matches_golden_tokens(name):
     steps = len(meta["tokens"])
     with torch.inference_mode():
         state = D.DecodeState(model, 1, len(prompt), steps)
+        runs = []
         for _ in range(2):  # a second pass checks that prefill resets state
             ids = torch.tensor([prompt], dtype=torch.int64, device="cuda")
             current = state.prefill(model, ids)
             tokens = list(D.stream_decode(state, current[:, 0].tolist(), steps))
-            check_tokens([t[0] for t in tokens], meta)
+            runs.append([t[0] for t in tokens])
             assert int(state.position) == len(prompt) + steps - 1
+    assert runs[0] == runs[1]
+    check_tokens(runs[0], meta, f"{name} graph decode")
 
 
 @pytest.mark.parametrize("name", ["tiny_decode", "qwen3_0.6b_decode"])
 def test_teacher_forced_decode_ids_match_oracle(name):
     """Every step of the captured decode graph, fed the oracle's own greedy
-    sequence, predicts the oracle's token (or one within DEFICIT of its max)."""
+    sequence, predicts the oracle's token, a near-tie, or a token the oracle's own
+    evaluation orders explain."""
     meta, _ = load(name)
     model = model_for(meta)
     prompt, golden = meta["prompt"], meta["tokens"]
     steps = len(golden)
-    shape = Q.SHAPES[meta["shape"]]
-    oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=meta["seed"]), meta["capacity"])
+    oracle = oracle_for(meta)
     logits = oracle.teacher_forced_logits(prompt, golden)
     with torch.inference_mode():
         state = D.DecodeState(model, 1, len(prompt), steps)
@@ -186,21 +193,12 @@ def test_teacher_forced_decode_ids_match_oracle(name):
             state.token.copy_(forced[i - 1:i].view(1, 1))
             state.graph.replay()
             preds.append(int(state.token))
-    exact = 0
-    for i, (p, g) in enumerate(zip(preds, golden)):
-        o = int(logits[i].to(torch.bfloat16).float().argmax())
-        # The oracle's batched teacher-forced pass agrees with its own
-        # token-by-token decode except at gaps below DEFICIT: its CPU GEMM and
-        # GEMV sum in different orders (on the 0.6B fixture they part at step
-        # 37, top-2 gap 0.0089, where the HIP path sides with the batched pass).
-        assert o == g or meta["top2_gap_fp32"][i] < DEFICIT
-        if p == o:
-            exact += 1
-        else:
-            deficit = float(logits[i].max()) - float(logits[i][p])
-            print(f"{name} step {i}: hip {p} vs oracle {o}, deficit {deficit:.4g}")
-            assert deficit < DEFICIT
-    print(f"{name}: {exact}/{steps} teacher-forced ids identical to the oracle's")
+    record = OP.TokenRecord()
+    for i, p in enumerate(preds):
+        record.add(i, logits[i], p)
+    o64 = Q.Oracle(oracle.shape, oracle.weights, oracle.capacity, acc=torch.float64)
+    check_record(record, f"{name} teacher-forced along the golden ids",
+                 OP.sequence_orders(oracle, o64, prompt, golden).callables())
 
 
 def test_engine_generate_repeated_prompts_and_speculation(tmp_path):
@@ -209,7 +207,7 @@ def test_engine_generate_repeated_prompts_and_speculation(tmp_path):
     steps = len(meta["tokens"])
     plain = Engine(path, speculative=False)
     out = [t[0] for t in plain.generate([meta["prompt"]], steps)]
-    check_tokens(out, meta)
+    check_tokens(out, meta, "tiny Engine.generate")
     other = Q.prompt_ids(5, 97, seed=3)
     assert len(list(plain.generate([other], 4))) == 4
     assert [t[0] for t in plain.generate([meta["prompt"]], steps)] == out

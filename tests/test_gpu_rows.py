@@ -111,8 +111,11 @@ def _tiles_abi(x, w, n, epilogue, residual=None, split=True):
 
 
 # Prompts of a few hundred rows split each tile's k range (the 8B down
-# projection at 256 and 300 rows, a 4B-wide O projection, a ragged width).
-SPLIT_CASES = [(256, 4096, 12288), (300, 2560, 4096), (260, 1000, 2048)]
+# projection at 256 and 300 rows, a 4B-wide O projection, a ragged width);
+# at 1024 rows the 8B O and down projections take 128-row tiles whose count
+# equals the 256 CUs, and split each tile's k range in two.
+SPLIT_CASES = [(256, 4096, 12288), (300, 2560, 4096), (260, 1000, 2048),
+               (1024, 4096, 4096), (1024, 4096, 12288)]
 
 
 @pytest.mark.parametrize("m,n,k", SPLIT_CASES)

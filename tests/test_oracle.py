@@ -206,3 +206,52 @@ def test_ops_fixture_reproduces():
     torch.testing.assert_close(n, t("add_norm", (4, 1024)), atol=1e-2, rtol=1e-2)
     w, xr = t("proj_w", (40, 1024)), t("proj_x", (1024,))
     torch.testing.assert_close(Q.linear(xr, w), t("proj_y", (40,)), atol=1e-2, rtol=1e-2)
+
+
+def test_float64_order_keeps_the_bf16_boundaries_and_differs_only_by_rounding():
+    """The float64 evaluation is the same formula: with inputs whose products
+    and sums are exact in both types it is bit-equal to the float32 one, and
+    on a model its logits stay within the float32 rounding noise."""
+    # Exact case: small integers times powers of two sum exactly in fp32.
+    x = torch.tensor([[1.0, 2.0, -3.0, 0.5]], dtype=BF16)
+    w = torch.tensor([[0.25, 1.0, 2.0, -4.0], [1.0, 1.0, 1.0, 1.0]], dtype=BF16)
+    shape = Q.Shape(hidden=4, layers=0, q_heads=1, kv_heads=1, head_dim=128, ffn=4,
+                    vocab=2, tied=False)
+    weights = {"lm_head": w, "embed": w, "norm": torch.ones(4, dtype=BF16)}
+    o32 = Q.Oracle(shape, weights, 4)
+    o64 = Q.Oracle(shape, weights, 4, acc=torch.float64)
+    assert torch.equal(o32._linear(x, "lm_head"), o64._linear(x, "lm_head"))
+    assert o64._dot(x, "lm_head").dtype == torch.float64
+    # A dropped bf16 rounding is not a different order: rms_norm keeps it.
+    v = Q.normal_bf16(6, 1, (3, 256), 1.0)
+    g = Q.normal_bf16(6, 2, (256,), 1.0)
+    n64 = Q.rms_norm(v, g, 1e-6, torch.float64)
+    vv = v.double()
+    unrounded = (g.double() * vv * torch.rsqrt(vv.square().mean(-1, keepdim=True) + 1e-6))
+    assert torch.equal(n64, (g.double() * (vv * torch.rsqrt(
+        vv.square().mean(-1, keepdim=True) + 1e-6)).to(BF16).double()).to(BF16))
+    assert not torch.equal(n64, unrounded.to(BF16))
+    # Whole model: float64 and float32 logits agree to the noise of fp32
+    # summation order through two bf16-rounded layers.
+    shape, weights = tiny()
+    prompt = Q.prompt_ids(9, shape.vocab, seed=4)
+    l32 = Q.Oracle(shape, weights, 16).teacher_forced_logits(prompt, [1, 2, 3])
+    l64 = Q.Oracle(shape, weights, 16, acc=torch.float64).teacher_forced_logits(prompt,
+                                                                               [1, 2, 3])
+    torch.testing.assert_close(l64, l32, atol=2e-2, rtol=0)
+    with pytest.raises(ValueError):
+        Q.Oracle(shape, weights, 16, acc=torch.float16)
+
+
+def test_stepwise_logits_equal_the_decode_loop():
+    """stepwise_logits is the oracle's own decode loop: the logits it returns
+    are those greedy_decode computes when fed the same tokens."""
+    shape, weights = tiny()
+    oracle = Q.Oracle(shape, weights, capacity=20)
+    prompt = Q.prompt_ids(6, shape.vocab, seed=5)
+    tokens, logits, _ = oracle.greedy_decode(prompt, 5)
+    stepwise = oracle.stepwise_logits(prompt, tokens)
+    for i in range(5):
+        assert torch.equal(stepwise[i], logits[i])
+    batched = oracle.teacher_forced_logits(prompt, tokens)
+    torch.testing.assert_close(batched, stepwise, atol=2e-2, rtol=0)

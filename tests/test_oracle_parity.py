@@ -78,12 +78,55 @@ def test_margin_is_half_a_pairwise_gap_where_bf16_is_fine():
             abs(OP.deficit(logits, 1) - d) < 1e-9
 
 
-def test_record_counts_and_bar():
-    rec = OP.TokenRecord(2e-2)
+def test_record_classifies_near_ties_noise_and_unexplained():
+    rec = OP.TokenRecord()                                # the 1e-3 near-tie bar
     rec.add(0, torch.tensor([0.0, -1.0, 0.5]), 2)        # identical
-    rec.add(1, torch.tensor([0.0, -0.015, -1.0]), 1)     # deficit 0.015 < bar
-    rec.add(2, torch.tensor([0.0, -0.05, -1.0]), 1)      # deficit 0.05, margin 0.025
-    s = rec.summary()
-    assert (s["checked"], s["identical"], s["over_bar"]) == (3, 1, 1)
-    assert abs(s["max_deficit"] - 0.05) < 1e-6
-    assert s["deficit_over_1e-3"] == 2
+    rec.add(1, torch.tensor([0.0, -0.0005, -1.0]), 1)    # deficit 5e-4: near-tie
+    rec.add(2, torch.tensor([0.0, -0.02, -1.0]), 1)      # needs other orders
+    rec.add(3, torch.tensor([0.0, -0.02, -1.0]), 1)
+    rec.add(4, torch.tensor([0.0, -0.02, -1.0]), 1)
+    assert rec.pending() == [2, 3, 4]
+    # Unexamined steps count as unexplained.
+    assert rec.summary()["unexplained"] == 3
+    other = {
+        2: torch.tensor([-0.001, 0.0, -1.0]),   # another order picks token 1
+        3: torch.tensor([0.0, -0.008, -1.0]),   # gaps 0.02 / 0.008: spread 0.012 >= 0.008
+        4: torch.tensor([0.0, -0.015, -1.0]),   # gaps 0.02 / 0.015: spread 0.005 < 0.015
+    }
+    calls = []
+
+    def order(step):
+        calls.append(step)
+        return other[step]
+
+    s = rec.explain({"other": order}).summary()
+    assert calls == [2, 3, 4]                   # only the pending steps are evaluated
+    assert (s["checked"], s["identical"], s["near_tie"], s["oracle_noise"],
+            s["unexplained"]) == (5, 1, 1, 2, 1)
+    assert abs(s["max_deficit"] - 0.02) < 1e-6
+    kinds = {d["step"]: d["kind"] for d in s["differing_steps"]}
+    assert kinds == {1: "near_tie", 2: "oracle_noise", 3: "oracle_noise", 4: "unexplained"}
+
+
+def test_near_tie_counts_the_bf16_rounding_of_the_decision():
+    # 2.0 and 2.0078125 round to the same bf16 value: id 0 wins the tie, and
+    # id 1, the fp32 maximum, has deficit 0: a near-tie whatever its margin.
+    kind, details = OP.classify(torch.tensor([2.0, 2.0078125]), 1, {})
+    assert kind == "near_tie" and details["deficit"] == 0.0
+    # A fp32 gap of 0.01 between logits in different bf16 buckets is no tie.
+    kind, _ = OP.classify(torch.tensor([2.01, 2.0]), 1, {})
+    assert kind == "unexplained"
+
+
+def test_orders_are_made_once_and_only_when_asked():
+    made = []
+
+    def maker():
+        made.append(1)
+        return torch.arange(12.0).view(4, 3)
+
+    orders = OP.Orders(x=maker).callables(offset=2)
+    assert made == []
+    assert orders["x"](3).tolist() == [3.0, 4.0, 5.0]
+    assert orders["x"](2).tolist() == [0.0, 1.0, 2.0]
+    assert made == [1]
