@@ -33,6 +33,12 @@ class Engine:
         self.speculative = speculative
         self.state = None
         self.speculator = None
+        self.reset_stats()
+
+    def reset_stats(self):
+        """Counters of the batch-one prompt-lookup loop: verify passes, draft
+        tokens proposed and accepted, and plain decode steps."""
+        self.stats = {"verify_passes": 0, "proposed": 0, "accepted": 0, "decode_steps": 0}
 
     def generate(self, input_ids: list, max_new_tokens: int):
         """Yield max_new_tokens lists of one greedy token per sequence.
@@ -76,6 +82,7 @@ class Engine:
             current = prefill(self.model, state, prompt)
             tokens = current[:, 0].tolist()
             if state.draft_tokens == 0:
+                self.stats["decode_steps"] += max_new_tokens - 1
                 yield from stream_decode(state, tokens, max_new_tokens)
                 return
             yield tokens
@@ -86,6 +93,9 @@ class Engine:
                 proposal = lookup.propose()
                 if proposal:
                     verified = state.verify(tokens[0], proposal, shape[1] + emitted - 1)
+                    self.stats["verify_passes"] += 1
+                    self.stats["proposed"] += len(proposal)
+                    self.stats["accepted"] += len(verified) - 1
                     # Scratch slots let a verify run at any position; emit only
                     # what the request still owes.
                     for token in verified[:max_new_tokens - emitted]:
@@ -95,6 +105,7 @@ class Engine:
                         yield tokens
                 else:
                     state.graph.replay()
+                    self.stats["decode_steps"] += 1
                     tokens = state.token[:, 0].tolist()
                     lookup.append(tokens[0])
                     emitted += 1

@@ -8,6 +8,7 @@ monotone), and hand-worked cases check ties and the halfway rounding.
 import itertools
 import random
 
+import pytest
 import torch
 
 from oracle import parity as OP
@@ -84,14 +85,16 @@ def test_record_classifies_near_ties_noise_and_unexplained():
     rec.add(1, torch.tensor([0.0, -0.0005, -1.0]), 1)    # deficit 5e-4: near-tie
     rec.add(2, torch.tensor([0.0, -0.02, -1.0]), 1)      # needs other orders
     rec.add(3, torch.tensor([0.0, -0.02, -1.0]), 1)
-    rec.add(4, torch.tensor([0.0, -0.02, -1.0]), 1)
+    rec.add(4, torch.tensor([0.0, -0.025, -1.0]), 1)
     assert rec.pending() == [2, 3, 4]
     # Unexamined steps count as unexplained.
     assert rec.summary()["unexplained"] == 3
     other = {
+        0: torch.tensor([0.0, -1.0, 0.5]),
+        1: torch.tensor([0.0, -0.0005, -1.0]),
         2: torch.tensor([-0.001, 0.0, -1.0]),   # another order picks token 1
         3: torch.tensor([0.0, -0.008, -1.0]),   # gaps 0.02 / 0.008: spread 0.012 >= 0.008
-        4: torch.tensor([0.0, -0.015, -1.0]),   # gaps 0.02 / 0.015: spread 0.005 < 0.015
+        4: torch.tensor([0.0, -0.015, -1.0]),   # gaps 0.025 / 0.015: spread 0.01 < 0.015
     }
     calls = []
 
@@ -100,12 +103,41 @@ def test_record_classifies_near_ties_noise_and_unexplained():
         return other[step]
 
     s = rec.explain({"other": order}).summary()
-    assert calls == [2, 3, 4]                   # only the pending steps are evaluated
+    # Every step is evaluated once a step is pending; the other order's only
+    # own flip (step 2, to token 1) has a primary deficit of 0.02, which
+    # admits no step with a larger deficit.
+    assert sorted(set(calls)) == [0, 1, 2, 3, 4]
+    assert abs(s["sequence_noise"] - 0.02) < 1e-6
     assert (s["checked"], s["identical"], s["near_tie"], s["oracle_noise"],
             s["unexplained"]) == (5, 1, 1, 2, 1)
-    assert abs(s["max_deficit"] - 0.02) < 1e-6
+    assert abs(s["max_deficit"] - 0.025) < 1e-6
     kinds = {d["step"]: d["kind"] for d in s["differing_steps"]}
     assert kinds == {1: "near_tie", 2: "oracle_noise", 3: "oracle_noise", 4: "unexplained"}
+    # Nothing pending: no order is evaluated.
+    quiet = OP.TokenRecord()
+    quiet.add(0, torch.tensor([0.0, -1.0]), 0)
+    quiet.explain({"other": lambda step: pytest.fail("evaluated without need")})
+
+
+def test_sequence_noise_admits_a_step_the_local_spread_does_not():
+    """A flip whose orders agree closely at its own position is oracle noise
+    when one of those orders itself flips, elsewhere on the sequence, to a
+    token at least as far below the primary's argmax."""
+    rec = OP.TokenRecord()
+    primary = [torch.tensor([0.0, -0.02, -1.0]), torch.tensor([0.0, -0.03, -1.0]),
+               torch.tensor([0.0, -0.5, -1.0])]
+    other = [torch.tensor([0.0, -0.021, -1.0]),   # local spread 0.001 < 0.02
+             torch.tensor([-0.01, 0.0, -1.0]),    # the order picks token 1 (deficit 0.03)
+             torch.tensor([0.0, -0.5, -1.0])]
+    for i, (l, t) in enumerate(zip(primary, (1, 0, 0))):
+        rec.add(i, l, t)
+    s = rec.explain({"other": lambda step: other[step]}).summary()
+    assert abs(s["sequence_noise"] - 0.03) < 1e-6
+    assert (s["oracle_noise"], s["unexplained"]) == (1, 0)
+    # The same flip alone (the order never flips) stays unexplained.
+    alone = OP.TokenRecord()
+    alone.add(0, primary[0], 1)
+    assert alone.explain({"other": lambda step: other[0]}).summary()["unexplained"] == 1
 
 
 def test_near_tie_counts_the_bf16_rounding_of_the_decision():
