@@ -44,6 +44,19 @@ static_assert(kCounterBytes == HTN_ATTENTION_COUNTER_BYTES, "counter region size
 // Pair p's 64-bit counter sits at the start of its 128-byte line; the XCD
 // mismatch count is the 32-bit word right after pair 0's counter.
 constexpr long kXcdMismatchByte = HTN_ATTENTION_XCD_MISMATCH_BYTE;
+// The fused output projection's words for pair p (at most 8 pairs) sit in
+// counter line kReadyLine + p, apart from the pair's arrival counter (the
+// output blocks poll them; polls on the counter's line slow its atomics):
+// the ready word (nonzero once every split of the pair has stored its
+// partial: 0x100 | the XCC_ID they ran on), and the count of the pair's
+// output blocks that have read it (the last one clears both). The word at
+// HTN_ATTENTION_OUTPUT_ERROR_BYTE of the region counts output blocks that
+// could not use their pair's partials (another XCD, or no arrival in time).
+constexpr int kReadyLine = 128, kReadyWord = 0, kReadersWord = 1;
+// Row block q's arrival count of pair partials: counter line kSumLine + q.
+constexpr int kSumLine = kReadyLine + 8;
+constexpr int kMaxOutputBlocks = kMaxCounterPairs - kSumLine;
+constexpr long kOutputErrorByte = HTN_ATTENTION_OUTPUT_ERROR_BYTE;
 static_assert(kXcdMismatchByte >= 8 && kXcdMismatchByte + 4 <= kCounterStride * 4,
               "mismatch word inside pair 0's line, past its counter");
 static_assert(48 < 64, "six bits per XCD hold up to 48 splits");
@@ -326,6 +339,19 @@ struct AttnArgs {
   const unsigned char* pf;
   long pf_units;
   int pf_unit_bytes, pf_per_class, attn_blocks;
+  // Output projection fused in (one sequence, in-kernel merge): o_blocks
+  // blocks per pair past the attention grid, on the pair's XCD, multiply the
+  // pair's columns of W_o (ow: [o_n, Hq D] bf16 or 8-bit, format o_fmt) by
+  // the pair's attention rows into fp32 partial rows ypart[pair][o_n].
+  const unsigned char* ow;
+  float* ypart;
+  int o_fmt, o_n, o_blocks, o_lpr;
+  // The last of a row block's pair partials sums them (in pair order),
+  // applies the 8-bit row scale, rounds, adds the residual res_o and rounds
+  // into out_o: bf16(bf16(sum) + residual) (projection.py:64-67).
+  const float* o_scale;
+  const bf16_t* res_o;
+  bf16_t* out_o;
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -475,6 +501,18 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
   }
   __syncthreads();
   if (!*last) return;
+  if (a.ow) {
+    // Fused output projection: the pair's output blocks merge the rows
+    // themselves. Every partial is in this XCD's L2; tell them so.
+    if (threadIdx.x == 0) {
+      unsigned xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      __hip_atomic_store(a.done + static_cast<long>(kReadyLine + p) * kCounterStride + kReadyWord,
+                         0x100u | (xcc & 0xffu), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   if (wave < R) {
     const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(prow, static_cast<uint32_t>(S) * D * 4);
     const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(mrow, static_cast<uint32_t>(S) * 8);
@@ -489,6 +527,242 @@ __device__ __forceinline__ void merge_tail(const AttnArgs& a, int b, int kvh, in
     *reinterpret_cast<uint32_t*>(dst) = pack_bf2(nx / den, ny / den);
   }
   if (threadIdx.x == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte agent-scope loads (see load_f2_sc1).
+__device__ __forceinline__ float4 load_f4_sc1(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                              uint32_t soff = 0) {
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 16);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                     __uint_as_float(v.w));
+}
+
+// v(lane) + v(lane ^ 32) in every lane (v_permlane32_swap of two copies).
+__device__ __forceinline__ float swap_sum32(float v) {
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// merge_row_short with 16-byte loads, two splits per wave instruction:
+// lanes 0-31 read split 2u, lanes 32-63 split 2u + 1, four dims per lane
+// (NP pairs cover 2 NP >= S splits); the halves' sums are added at the end,
+// so lane l < 32 holds dims 4 l .. 4 l + 3 of the row. Half the load
+// instructions of merge_row_short (8B decode step 2.789 -> 2.772 ms with the
+// fused output projection, whose blocks merge after the last split lands).
+template <int NP>
+__device__ __forceinline__ void merge_row_wide(__amdgpu_buffer_rsrc_t prs, __amdgpu_buffer_rsrc_t mrs,
+                                               int S, int lane, float4& num, float& den) {
+  const uint32_t half = static_cast<uint32_t>(lane) >> 5;
+  const uint32_t lo = (static_cast<uint32_t>(lane) & 31u) * 16u + half * D * 4;
+  const float2 ml = load_f2_sc1(mrs, static_cast<uint32_t>(lane) * 8);
+  float4 pv[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) pv[u] = load_f4_sc1(prs, lo, u * 2 * D * 4);
+  __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first wait
+  const float M = wave_max(lane < S ? ml.x : -INFINITY);
+  const float w = lane < S && ml.x != -INFINITY ? expf(ml.x - M) : 0.f;
+  den = wave_sum(w * ml.y);
+  float4 n = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const float w0 = readlane(w, 2 * u), w1 = readlane(w, 2 * u + 1);
+    const float wu = half ? w1 : w0;
+    n.x = fmaf(wu, pv[u].x, n.x);
+    n.y = fmaf(wu, pv[u].y, n.y);
+    n.z = fmaf(wu, pv[u].z, n.z);
+    n.w = fmaf(wu, pv[u].w, n.w);
+  }
+  num = make_float4(swap_sum32(n.x), swap_sum32(n.y), swap_sum32(n.z), swap_sum32(n.w));
+}
+
+// The merged row r of pair p (one wave), merge_tail's formula, into `arow`
+// (64 words, word i holding the bf16 pair of dims 2 i, 2 i + 1).
+__device__ __forceinline__ void merge_row_to(const AttnArgs& a, int p, int r, int lane,
+                                             uint32_t* arow) {
+  const int R = a.G * a.Q, S = a.splits;
+  const long orow = static_cast<long>(p) * R + r;
+  const __amdgpu_buffer_rsrc_t prs =
+      uniform_rsrc(a.part + orow * S * D, static_cast<uint32_t>(S) * D * 4);
+  const __amdgpu_buffer_rsrc_t mrs = uniform_rsrc(a.ml + orow * S * 2, static_cast<uint32_t>(S) * 8);
+  // The host fuses the projection for at most kOMaxSplits splits, which
+  // keeps the merge's loads and the block's weights within the registers.
+  float4 nm;
+  float den;
+  if (S <= 8) merge_row_wide<4>(prs, mrs, S, lane, nm, den);
+  else if (S <= 16) merge_row_wide<8>(prs, mrs, S, lane, nm, den);
+  else merge_row_wide<12>(prs, mrs, S, lane, nm, den);
+  if (lane < 32) {
+    arow[2 * lane] = pack_bf2(nm.x / den, nm.y / den);
+    arow[2 * lane + 1] = pack_bf2(nm.z / den, nm.w / den);
+  }
+}
+
+// The fused output projection (one sequence): block o past the attention
+// grid serves pair p = o % 8 (the XCD column of the pair's splits) and
+// output rows [128 (o / 8), + 128). Each lane group of 16 lanes owns one row
+// at a time: lane j holds bytes 16 j + 256 c (c < LPR) of the row's span of
+// the pair's columns (G D weights), eight rows per group, all 8 LPR 16-byte
+// loads issued at once, before the wait. When the pair's last split has
+// stored its partial, the block merges the pair's G attention rows (the
+// bf16 rows the unfused kernel writes, merge_tail's arithmetic) into LDS,
+// takes its dot products, reduces each over the 16 lanes and stores the fp32
+// row sums to ypart[p][row]. The pair's partial over its columns is summed
+// with the other pairs', scaled, rounded and added to the residual by
+// output_partials_residual.
+constexpr int kORowsPerGroup = 8;
+// Smallest output projection worth fusing: the fusion wins on the 8B decode
+// step (33.6 MB: 2.841 -> 2.782 ms per step), breaks even at 16.8 MB (8B int8
+// 462.3 -> 462.5 tok/s, fp8 471.7 -> 473.7), and loses on the 0.6B shape
+// (4.2 MB: 0.660 -> 0.693 ms), where the projection is short anyway.
+constexpr long kFuseMinBytes = 16L << 20;
+constexpr int kOMaxSplits = 24;
+constexpr int kORowsPerBlock = 4 * 4 * kORowsPerGroup;  // 128
+constexpr int kOMaxPolls = 1 << 16;
+
+template <int WF, int LPR>
+__device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) {
+  constexpr int kB = Fmt<WF>::kBytes;
+  constexpr int kXW = WF == WF_BF16 ? 4 : 8;  // activation words per 16-byte weight load
+  const int o = static_cast<int>(blockIdx.x) - a.attn_blocks;
+  const int p = o & 7, q = o >> 3;
+  if (p >= a.Hkv) return;  // no pair on this XCD column
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  unsigned* line = a.done + static_cast<long>(kReadyLine + p) * kCounterStride;
+  // 1. The block's weights, all in flight at once (rows past o_n read zeros),
+  // issued about a microsecond after the attention blocks' first K/V loads
+  // (8B decode step at context 2048: 2.817 -> 2.798 ms; two microseconds
+  // gave 2.815).
+  __builtin_amdgcn_s_sleep(40);
+  const uint32_t row_bytes = static_cast<uint32_t>(a.Hq) * D * kB;
+  const __amdgpu_buffer_rsrc_t wrs =
+      buffer_rsrc(a.ow, static_cast<uint32_t>(a.o_n) * row_bytes);
+  const uint32_t col0 = static_cast<uint32_t>(p * a.G * D * kB) + 16u * j;
+  const int row0 = q * kORowsPerBlock + wave * 4 * kORowsPerGroup + g;
+  uint4 w[kORowsPerGroup][LPR];
+#pragma unroll
+  for (int it = 0; it < kORowsPerGroup; ++it) {
+    const uint32_t voff = static_cast<uint32_t>(row0 + 4 * it) * row_bytes + col0;
+#pragma unroll
+    for (int c = 0; c < LPR; ++c) w[it][c] = buffer_load16_stream(wrs, voff + 256u * c, 0);
+  }
+  // 2. Wait for the pair's splits (wave 0 polls, bounded).
+  __shared__ unsigned ready;
+  if (wave == 0) {
+    unsigned v = 0;
+    for (int i = 0; i < kOMaxPolls; ++i) {
+      v = __hip_atomic_load(line + kReadyWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    if (lane == 0) ready = v;
+  }
+  __syncthreads();
+  const unsigned rv = ready;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (rv == 0 || (rv & 0xffu) != (xcc & 0xffu)) {
+    // The partials are not visible here: leave the rows unwritten and count
+    // the failure for the host.
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(a.done + kOutputErrorByte / 4, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  // 3. The pair's attention rows into LDS, then this block is done with the
+  // ready word: the last of the pair's output blocks clears it.
+  const int R = a.G;
+  if (wave < R) merge_row_to(a, p, wave, lane, alds + wave * (D / 2));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned n =
+        __hip_atomic_fetch_add(line + kReadersWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    if (n == static_cast<unsigned>(a.o_blocks)) {
+      __hip_atomic_store(line + kReadersWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(line + kReadyWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // 4. Dot products: weight byte 16 j + 256 c of the span is column
+  // (16 j + 256 c) / kB of the pair, whose bf16 activation sits at byte
+  // 2 (16 j + 256 c) / kB of the staged rows.
+  uint32_t x[LPR][kXW];
+#pragma unroll
+  for (int c = 0; c < LPR; ++c) {
+    const uint32_t* src = alds + (2 * (16 * j + 256 * c) / kB) / 4;
+#pragma unroll
+    for (int u = 0; u < kXW; ++u) x[c][u] = src[u];
+  }
+  // 5. The fp32 row sums go out through cache-bypassing (agent-scope atomic)
+  // stores, so the block that completes this row block, on whichever XCD,
+  // reads them from the coherent level: the protocol of AMD's rocPRIM
+  // look-back scan on gfx942/gfx950 (atomic stores and loads of the data,
+  // order-only fences, an atomic counter), with no L2 write-back.
+  unsigned* yrow = reinterpret_cast<unsigned*>(a.ypart + static_cast<long>(p) * a.o_n);
+#pragma unroll
+  for (int it = 0; it < kORowsPerGroup; ++it) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < LPR; ++c) s = dot_vec<WF>(w[it][c], x[c], s);
+    s = row16_sum(s);
+    const int row = row0 + 4 * it;
+    if (j == 0 && row < a.o_n)
+      __hip_atomic_store(yrow + row, __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ unsigned last_pair;
+  if (threadIdx.x == 0) {
+    unsigned* cnt = a.done + static_cast<long>(kSumLine + q) * kCounterStride;
+    const unsigned n =
+        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    last_pair = n == static_cast<unsigned>(a.Hkv);
+    if (n == static_cast<unsigned>(a.Hkv))
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_pair) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  // 6. This block completed row block q: every pair's partial rows are
+  // stored; sum them for rows [128 q, 128 q + 128).
+  const int t = threadIdx.x;
+  const int row = q * kORowsPerBlock + t;
+  if (t < kORowsPerBlock && row < a.o_n) {
+    const unsigned* yall = reinterpret_cast<const unsigned*>(a.ypart);
+    float v[8];
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp)
+      v[pp] = pp < a.Hkv ? __uint_as_float(__hip_atomic_load(
+                               yall + static_cast<long>(pp) * a.o_n + row, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT))
+                         : 0.f;
+    float sum = v[0];
+#pragma unroll
+    for (int pp = 1; pp < 8; ++pp) sum += v[pp];
+    if (a.o_scale) sum *= a.o_scale[row];
+    a.out_o[row] = static_cast<bf16_t>(f2bf(round_bf(sum) + bf2f(a.res_o[row])));
+  }
+}
+
+// Dispatch on the weight format and the span's 16-byte loads per lane.
+__device__ __forceinline__ void output_role(const AttnArgs& a, uint32_t* alds) {
+  if (a.o_fmt == WF_BF16) {
+    if (a.o_lpr == 4) output_block<WF_BF16, 4>(a, alds);
+    else if (a.o_lpr == 2) output_block<WF_BF16, 2>(a, alds);
+    else output_block<WF_BF16, 1>(a, alds);
+  } else if (a.o_fmt == WF_INT8) {
+    if (a.o_lpr == 4) output_block<WF_INT8, 4>(a, alds);
+    else if (a.o_lpr == 2) output_block<WF_INT8, 2>(a, alds);
+    else output_block<WF_INT8, 1>(a, alds);
+  } else {
+    if (a.o_lpr == 4) output_block<WF_FP8, 4>(a, alds);
+    else if (a.o_lpr == 2) output_block<WF_FP8, 2>(a, alds);
+    else output_block<WF_FP8, 1>(a, alds);
+  }
 }
 
 // The block's result per query row of the LDS-staged kernels, one wave per
@@ -1142,13 +1416,16 @@ __device__ __forceinline__ void read_tile(uint32_t addr, uint4 (&ko)[4], uint4 (
   }
 }
 
-template <int ROWS, int PRO, int RING>
+template <int ROWS, int PRO, int RING, bool OUT>
 __global__ __launch_bounds__(kBlock) void attention_lds(AttnArgs a) {
+  // OUT: the launch carries the fused output projection's blocks (their
+  // weights stay in registers, so only those launches pay for them).
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
   preload_args<FUSED>(a);
-  if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
-    prefetch_next(a, ring);
+  if ((a.pf || a.ow) && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
+    if constexpr (OUT) output_role(a, reinterpret_cast<uint32_t*>(ring));
+    else prefetch_next(a, ring);
     return;
   }
   __shared__ uint32_t qs[ROWS * D / 2];
@@ -1487,13 +1764,14 @@ __device__ __forceinline__ void read_tile_mf(const uint32_t (&kaddr)[4], const u
   k[3] = make_uint4(k3.x, k3.y, k3.z, k3.w);
 }
 
-template <int ROWS, int PRO, int RING>
+template <int ROWS, int PRO, int RING, bool OUT>
 __global__ __launch_bounds__(kBlock) void attention_mfma(AttnArgs a) {
   constexpr bool FUSED = PRO != PRO_NONE;
   extern __shared__ __align__(16) unsigned char ring[];  // RING tiles of K/V staging
   preload_args<FUSED>(a);
-  if (a.pf && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
-    prefetch_next(a, ring);
+  if ((a.pf || a.ow) && static_cast<int>(blockIdx.x) >= a.attn_blocks) {
+    if constexpr (OUT) output_role(a, reinterpret_cast<uint32_t*>(ring));
+    else prefetch_next(a, ring);
     return;
   }
   // MQ: several queries per sequence (16 or 32 rows = heads x queries, each
@@ -2193,7 +2471,8 @@ namespace {
 dim3 split_grid(const AttnArgs& a) {
   if (!a.done) return dim3(a.splits, a.Hkv, a.B);
   const long pairs = static_cast<long>(a.B) * a.Hkv;
-  return dim3(static_cast<unsigned>(8 * ((pairs + 7) / 8) * a.splits + (a.pf ? 8 * a.pf_per_class : 0)));
+  return dim3(static_cast<unsigned>(8 * ((pairs + 7) / 8) * a.splits +
+                                    (a.pf ? 8 * a.pf_per_class : 0) + (a.ow ? 8 * a.o_blocks : 0)));
 }
 
 template <int ROWS, int TILES>
@@ -2218,28 +2497,45 @@ void launch_stream(bool fused, const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attention_stream<ROWS, PRO_ROW>), grid, dim3(kBlock), 0, st, a);
 }
 
-template <int ROWS, int PRO, int RING>
-void launch_lds_t(const AttnArgs& a, hipStream_t st) {
+template <int ROWS, int PRO, int RING, bool OUT>
+void launch_lds_o(const AttnArgs& a, hipStream_t st) {
   const size_t lds = static_cast<size_t>(RING) * kLdsTile;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&attention_lds<ROWS, PRO, RING>),
+      reinterpret_cast<const void*>(&attention_lds<ROWS, PRO, RING, OUT>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   (void)attr;  // a refused size surfaces as a launch error
-  hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
+  hipLaunchKernelGGL((attention_lds<ROWS, PRO, RING, OUT>), split_grid(a), dim3(kBlock), lds, st, a);
 }
 
+// The fused output projection only runs with the fused prologue.
 template <int ROWS, int PRO, int RING>
-void launch_mfma_t(const AttnArgs& a, hipStream_t st) {
+void launch_lds_t(const AttnArgs& a, hipStream_t st) {
+  if constexpr (PRO != PRO_NONE) {
+    if (a.ow) return launch_lds_o<ROWS, PRO, RING, true>(a, st);
+  }
+  launch_lds_o<ROWS, PRO, RING, false>(a, st);
+}
+
+template <int ROWS, int PRO, int RING, bool OUT>
+void launch_mfma_o(const AttnArgs& a, hipStream_t st) {
   // The ring, which with several queries (ROWS > 8) the waves' partial states
   // reuse after the last tile.
   constexpr size_t kStates = ROWS > 8 ? static_cast<size_t>(kBlock / kWave) * ROWS * D * 4 : 0;
   const size_t lds = static_cast<size_t>(RING) * kLdsTile > kStates ? static_cast<size_t>(RING) * kLdsTile
                                                                      : kStates;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&attention_mfma<ROWS, PRO, RING>),
+      reinterpret_cast<const void*>(&attention_mfma<ROWS, PRO, RING, OUT>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   (void)attr;  // a refused size surfaces as a launch error
-  hipLaunchKernelGGL((attention_mfma<ROWS, PRO, RING>), split_grid(a), dim3(kBlock), lds, st, a);
+  hipLaunchKernelGGL((attention_mfma<ROWS, PRO, RING, OUT>), split_grid(a), dim3(kBlock), lds, st, a);
+}
+
+template <int ROWS, int PRO, int RING>
+void launch_mfma_t(const AttnArgs& a, hipStream_t st) {
+  if constexpr (PRO != PRO_NONE) {
+    if (a.ow) return launch_mfma_o<ROWS, PRO, RING, true>(a, st);
+  }
+  launch_mfma_o<ROWS, PRO, RING, false>(a, st);
 }
 
 // Several queries per sequence (verify rows): 16 or 32 query rows per kv head.
@@ -2347,6 +2643,19 @@ struct NextWeights {
   int format;
 };
 
+// The output projection fused into the attention launch (one sequence): its
+// weights (n rows of k = Hq D weights, format 0 bf16 or 8-bit) and the fp32
+// partial rows [Hkv, n] the output blocks write.
+struct FusedOutput {
+  const void* w;
+  long n, k;
+  int format;
+  float* ypart;
+  const float* scale;
+  const bf16_t* res;
+  bf16_t* out;
+};
+
 // Prefetch blocks per XCD, and the bytes they read into each XCD's 4 MB L2
 // (measured on 0.6B and 8B decode steps: 8 blocks beat 2, 4, 16 and 32 -- few
 // blocks outlast the attention, many crowd its loads -- and 3 MB per XCD beat
@@ -2395,7 +2704,7 @@ int run_prefill_attention(AttnArgs& a, hipStream_t st) {
 }
 
 int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
-                  const NextWeights* next = nullptr) {
+                  const NextWeights* next = nullptr, const FusedOutput* fo = nullptr) {
   const int rows = a.G * a.Q;
   if (rows <= 0 || rows > kMaxRows || a.Q > kMaxQ || a.B <= 0 || a.Hkv <= 0 || a.cap <= 0)
     return HTN_EUNSUPPORTED;
@@ -2478,13 +2787,40 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
       out_pairs && xcd_affine_merge(st))
     a.done = reinterpret_cast<unsigned*>(sbase);
   a.scale = 1.0f / sqrtf(static_cast<float>(D));
+  // The output projection in the same launch: one sequence on the
+  // XCD-affine grid of the staged kernels (each kv head's splits on one XCD),
+  // merged by the output blocks from at most kOMaxSplits partials, with the
+  // pair's span of each weight row a whole number (1, 2 or 4) of 256-byte
+  // pieces and 32-bit byte offsets over the weights.
+  a.ow = nullptr;
+  a.ypart = nullptr;
+  if (fo && fo->w && fo->ypart && a.done && a.ring > 0 && !a.stream && a.B == 1 && a.Q == 1 &&
+      a.Hkv <= 8 && a.splits <= kOMaxSplits && fo->k == static_cast<long>(a.Hq) * D) {
+    const long kb = fo->format == 0 ? 2 : 1;
+    const long span = static_cast<long>(a.G) * D * kb;
+    const long lpr = span / 256;
+    if (span % 256 == 0 && (lpr == 1 || lpr == 2 || lpr == 4) && fo->n > 0 &&
+        fo->n * fo->k * kb < (1L << 31) && fo->n * fo->k * kb >= kFuseMinBytes) {
+      a.ow = static_cast<const unsigned char*>(fo->w);
+      a.ypart = fo->ypart;
+      a.o_fmt = fo->format;
+      a.o_n = static_cast<int>(fo->n);
+      a.o_lpr = static_cast<int>(lpr);
+      a.o_blocks = static_cast<int>((fo->n + kORowsPerBlock - 1) / kORowsPerBlock);
+      a.attn_blocks = static_cast<int>(8 * a.splits);  // one pair per XCD column
+      a.o_scale = fo->format != 0 ? fo->scale : nullptr;
+      a.res_o = fo->res;
+      a.out_o = fo->out;
+      if (a.o_blocks > kMaxOutputBlocks) a.ow = nullptr;
+    }
+  }
   // Prefetch of the next projection's weights: only with the XCD-affine grid
   // of the LDS-staged kernels (one dimension, eight block columns) and a
   // GEMV grid of whole columns, so span u and its GEMV block share an XCD.
   a.pf = nullptr;
   long gemv_blocks = 0;
   int gemv_rows = 0;
-  if (next && next->w && a.done && a.ring > 0 && !a.stream &&
+  if (next && next->w && !a.ow && a.done && a.ring > 0 && !a.stream &&
       gemv_plain_layout(next->n, next->k, next->format, &gemv_blocks, &gemv_rows) &&
       gemv_blocks % 8 == 0) {
     const long row_bytes = next->k * (next->format == 0 ? 2 : 1);
@@ -2589,7 +2925,8 @@ int prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v
                        int rope_by_position, void* keys, void* values, int64_t cap,
                        const int64_t* positions, void* out, int64_t B, int64_t Hkv,
                        int64_t groups, void* scratch, const NextWeights* next,
-                       htn_stream_t stream) {
+                       htn_stream_t stream, const FusedOutput* fo = nullptr,
+                       bool* fused_output = nullptr) {
   if (!qkv || !q_gain || !k_gain || !cos || !sin || !keys || !values || !positions || !out)
     return HTN_EINVAL;
   if (Hkv <= 0 || groups <= 0 || rope_rows <= 0) return HTN_EINVAL;
@@ -2609,7 +2946,9 @@ int prologue_attention(const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v
   a.B = static_cast<int>(B); a.Hkv = static_cast<int>(Hkv); a.G = static_cast<int>(groups);
   a.Hq = static_cast<int>(Hkv * groups); a.Q = 1;
   a.o_sh = D; a.o_st = D; a.o_sb = static_cast<long>(a.Hq) * D;  // out [B, Hq, 128]
-  return run_attention(true, a, scratch, static_cast<hipStream_t>(stream), next);
+  const int rc = run_attention(true, a, scratch, static_cast<hipStream_t>(stream), next, fo);
+  if (fused_output) *fused_output = a.ow != nullptr;
+  return rc;
 }
 }  // namespace
 
@@ -2640,6 +2979,66 @@ extern "C" int htn_prologue_attention_prefetch(
   return prologue_attention(qkv, qkv_sb, k_off, v_off, q_gain, k_gain, q_eps, k_eps, cos, sin,
                             rope_st, rope_rows, rope_by_position, keys, values, cap, positions,
                             out, B, Hkv, groups, scratch, &next, stream);
+}
+
+namespace {
+// Scratch of htn_prologue_attention_output: the attention's (counters, then
+// split partials), the fp32 partial rows of the fused output projection, and
+// the attention rows of the unfused fallback.
+long output_scratch_layout(long B, long Hq, long Hkv, long cap, long n, long* ypart_off,
+                           long* rows_off) {
+  const long base = (htn_attention_scratch_bytes(B, Hq, 1, cap) + 255) / 256 * 256;
+  *ypart_off = base;
+  *rows_off = base + (B * Hkv * n * 4 + 255) / 256 * 256;
+  return *rows_off + B * Hq * D * 2;
+}
+}  // namespace
+
+extern "C" int64_t htn_attention_output_scratch_bytes(int64_t B, int64_t Hq, int64_t Hkv,
+                                                      int64_t cap, int64_t n) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || cap <= 0 || n <= 0) return 0;
+  long yo = 0, ro = 0;
+  return output_scratch_layout(B, Hq, Hkv, cap, n, &yo, &ro);
+}
+
+extern "C" int htn_prologue_attention_output(
+    const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off, const void* q_gain,
+    const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+    int64_t rope_st, int64_t rope_rows, int rope_by_position, void* keys, void* values,
+    int64_t cap, const int64_t* positions, int64_t B, int64_t Hkv, int64_t groups,
+    const void* o_weight, const float* o_scale, int o_format, int64_t n,
+    const void* residual, void* out, void* scratch, htn_stream_t stream) {
+  if (!o_weight || !residual || !out || !scratch || n <= 0 || B <= 0 || Hkv <= 0 || groups <= 0)
+    return HTN_EINVAL;
+  if (o_format != 0 && o_format != HTN_WEIGHT_INT8 && o_format != HTN_WEIGHT_FP8_E4M3)
+    return HTN_EINVAL;
+  if (o_format != 0 && !o_scale) return HTN_EINVAL;
+  const long Hq = Hkv * groups, k = Hq * D;
+  long yo = 0, ro = 0;
+  output_scratch_layout(B, Hq, Hkv, cap, n, &yo, &ro);
+  unsigned char* sb = static_cast<unsigned char*>(scratch);
+  float* ypart = reinterpret_cast<float*>(sb + yo);
+  bf16_t* rows = reinterpret_cast<bf16_t*>(sb + ro);
+  const FusedOutput fo{o_weight, n, k, o_format, ypart, o_scale,
+                       static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(out)};
+  // Unfused, the attention's idle CUs still prefetch W_o into L2.
+  const NextWeights next{o_weight, n, k, o_format};
+  bool fused = false;
+  int rc = prologue_attention(qkv, qkv_sb, k_off, v_off, q_gain, k_gain, q_eps, k_eps, cos, sin,
+                              rope_st, rope_rows, rope_by_position, keys, values, cap, positions,
+                              rows, B, Hkv, groups, scratch, &next, stream, &fo, &fused);
+  if (rc != HTN_OK) return rc;
+  if (fused) return HTN_OK;  // the launch wrote `out`
+  // Unfused: the attention rows went to scratch; the residual GEMV follows.
+  for (long b = 0; b < B; ++b) {
+    const bf16_t* x = rows + b * k;
+    const bf16_t* r = static_cast<const bf16_t*>(residual) + b * n;
+    bf16_t* y = static_cast<bf16_t*>(out) + b * n;
+    rc = o_format == 0 ? htn_gemv_residual(x, o_weight, r, y, n, k, stream)
+                       : htn_gemv_residual_w8(x, o_weight, o_scale, o_format, r, y, n, k, stream);
+    if (rc != HTN_OK) return rc;
+  }
+  return HTN_OK;
 }
 
 extern "C" int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream) {

@@ -22,59 +22,6 @@ namespace htn {
 
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
-// Weight storage: bf16, or one byte per weight (int8 two's complement, or OCP
-// fp8 e4m3fn) with an fp32 scale per output row.
-enum WeightFormat { WF_BF16 = 0, WF_INT8 = HTN_WEIGHT_INT8, WF_FP8 = HTN_WEIGHT_FP8_E4M3 };
-
-template <int WF>
-struct Fmt {
-  static constexpr int kBytes = WF == WF_BF16 ? 2 : 1;  // bytes per weight
-  static constexpr int kPerVec = 16 / kBytes;           // weights per 16-byte load
-};
-
-// Two fp32 values that are exact in bf16 (small integers) packed as bf16.
-__device__ __forceinline__ uint32_t pack_exact_bf2(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-// Partial dot product of one 16-byte weight vector with its activations,
-// which stay packed bf16 pairs (xp[i] holds activations 2i, 2i+1). Every
-// weight is first made an exact bf16 value, so each step is one bf16 dot2:
-//  bf16: 8 weights, used as loaded.
-//  int8: 16 weights; each byte converts to fp32 with sign extension in the
-//        conversion itself (exact), two values pack into one bf16 pair.
-//  fp8:  16 weights; the hardware converts two e4m3fn codes straight to a
-//        bf16 pair (gfx950 decodes OCP e4m3fn; every e4m3 value is a bf16
-//        value, and the unit scale leaves it unchanged).
-template <int WF>
-__device__ __forceinline__ float dot_vec(uint4 w, const uint32_t* xp, float s) {
-  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-  if constexpr (WF == WF_BF16) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s = dot2(d[j], xp[j], s);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t p0, p1;
-      if constexpr (WF == WF_INT8) {
-        const int v = static_cast<int>(d[j]);
-        p0 = pack_exact_bf2(static_cast<float>(static_cast<signed char>(v)),
-                            static_cast<float>(static_cast<signed char>(v >> 8)));
-        p1 = pack_exact_bf2(static_cast<float>(static_cast<signed char>(v >> 16)),
-                            static_cast<float>(v >> 24));
-      } else {
-        p0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                                              static_cast<int>(d[j]), 1.0f, false));
-        p1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                                              static_cast<int>(d[j]), 1.0f, true));
-      }
-      s = dot2(p0, xp[2 * j], s);
-      s = dot2(p1, xp[2 * j + 1], s);
-    }
-  }
-  return s;
-}
-
 // LDS layout: [0, 64) argmax keys of the four waves, [64, 128) reduction
 // scratch, then the staged activation row.
 constexpr int kLdsHead = 128;

@@ -5,9 +5,11 @@ forward (78-99), DecodeState (102-206) and stream_decode (8-22), with the
 same device-resident token/position state so a captured step replays
 without host involvement. The batch-one step is five HIP kernels per layer:
 
-  gemv_norm(ln1, W_qkv) -> decode attention (QK-norm, RoPE from the table at
-  the device position, KV append, split-KV softmax and merge) ->
-  gemv_residual(W_o) -> gemv_norm_swiglu(ln2, W_gate_up) -> gemv_residual(W_down)
+  gemv_norm(ln1, W_qkv) -> decode attention with the output projection
+  (QK-norm, RoPE from the step's row, KV append, split-KV softmax; each kv
+  head's XCD merges its heads and multiplies their columns of W_o) -> the
+  partials' sum + residual -> gemv_norm_swiglu(ln2, W_gate_up) ->
+  gemv_residual(W_down)
 
 plus one embedding gather before the layers and one fused
 final-norm/LM-head/argmax kernel after them, which also writes the token and
@@ -17,7 +19,7 @@ import torch
 
 from ._lib import HEAD_DIM
 from .kernels.attention import (check_xcd_merge, decode_attention, grouped_attention,
-                                prologue_attention)
+                                prologue_attention_output)
 from .kernels.down import down_residual
 from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
@@ -109,15 +111,16 @@ def decode_layer(model, i, h, cache, position, rotary, rope=None):
     ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
     packed = norm_projection(h, ln1.weight, layer.qkv_weight, ln1.variance_epsilon)
     if rope is not None:
-        a = prologue_attention(packed, layer.q_norm, layer.k_norm, rope[0], rope[1],
-                               cache.keys[i], cache.values[i], position,
-                               c.num_key_value_heads, groups, q_width, q_width + k_width,
-                               next_weight=layer.o_weight)
+        # Attention and the output projection with its residual in one call.
+        r = prologue_attention_output(packed, layer.q_norm, layer.k_norm, rope[0], rope[1],
+                                      cache.keys[i], cache.values[i], position,
+                                      c.num_key_value_heads, groups, q_width,
+                                      q_width + k_width, layer.o_weight, h)
     else:
         a = decode_attention(packed, layer.q_norm, layer.k_norm, cos[0], sin[0],
                              cache.keys[i], cache.values[i], position,
                              c.num_key_value_heads, groups, q_width, q_width + k_width)
-    r = output_projection_residual(a, layer.o_weight, h)
+        r = output_projection_residual(a, layer.o_weight, h)
     m = norm_projection(r, ln2.weight, layer.gate_up_weight, ln2.variance_epsilon,
                         swiglu=True)
     return down_residual(m, layer.down_weight, r)

@@ -16,15 +16,19 @@ from ..quant import QuantizedWeight
 _SCRATCH = {}
 
 
-def _scratch(device, batch, heads, queries, capacity):
+def _scratch(device, batch, heads, queries, capacity, nbytes=None):
     """The attention scratch of the current stream. Its leading arrival
     counters must be zero before a call and every call leaves them zero, so
     one zero-filled buffer per stream is kept and reused (calls on one stream
     are ordered; buffers of different streams never meet). It only grows, and
     outgrown buffers are kept: a captured graph may still use their address.
     During capture a too-small buffer is not replaced: the call gets a fresh
-    zero-filled one, whose fill the graph records ahead of the kernel."""
-    nbytes = max(_lib.load().htn_attention_scratch_bytes(batch, heads, queries, capacity), 4)
+    zero-filled one, whose fill the graph records ahead of the kernel.
+    `nbytes` overrides the attention's own size (the fused output projection
+    needs more)."""
+    if nbytes is None:
+        nbytes = _lib.load().htn_attention_scratch_bytes(batch, heads, queries, capacity)
+    nbytes = max(nbytes, 4)
     current = torch.cuda.current_stream(device)
     buffers = _SCRATCH.setdefault((current.device_index, current.cuda_stream), [])
     if buffers and buffers[-1].numel() * 4 >= nbytes:
@@ -37,23 +41,24 @@ def _scratch(device, batch, heads, queries, capacity):
 
 def xcd_merge_mismatches(device=None, reset=False):
     """How many in-kernel split merges found a split of their (batch, kv head)
-    pair on another XCD than their own, summed over the attention scratch
-    buffers kept for `device` (0 on a correct run: the merge relies on
+    pair on another XCD than their own, plus how many fused output-projection
+    blocks could not use their pair's partials, summed over the attention
+    scratch buffers kept for `device` (0 on a correct run: both rely on
     round-robin workgroup dispatch to keep a pair's partials in one L2).
     Reads device memory, so it synchronises; reset=True clears the counts."""
     index = torch.device(device).index if device is not None else torch.cuda.current_device()
     if index is None:
         index = torch.cuda.current_device()
-    word = _lib.ATTENTION_XCD_MISMATCH_BYTE // 4
+    words = [_lib.ATTENTION_XCD_MISMATCH_BYTE // 4, _lib.ATTENTION_OUTPUT_ERROR_BYTE // 4]
     total = 0
     for (dev, _stream), buffers in _SCRATCH.items():
         if dev != index:
             continue
         for buffer in buffers:
-            count = buffer.view(torch.int32)[word]
-            total += int(count)
+            counts = buffer.view(torch.int32)[words[0]:words[1] + 1]
+            total += int(counts.sum())
             if reset:
-                count.zero_()
+                counts.zero_()
     return total
 
 
@@ -154,6 +159,53 @@ def _prologue(qkv, q_norm, k_norm, cos, sin, by_position, keys, values, position
     _lib.require_gpu(data)
     _lib.call("htn_prologue_attention_prefetch", *args, _lib.ptr(data), data.shape[0],
               data.shape[1], fmt, _lib.stream(qkv.device))
+    return out
+
+
+def prologue_attention_output(qkv, q_norm, k_norm, cos, sin, keys, values, positions,
+                              kv_heads, groups, k_offset, v_offset, o_weight, residual):
+    """prologue_attention followed by output_projection_residual(a, o_weight,
+    residual) (attention.py:162 then projection.py:70, as fused_layer.py:146-147
+    runs them), in one library call: for one sequence the projection runs in
+    the attention launch (each kv head's XCD multiplies that head group's
+    columns of W_o while the attention runs) plus a small summing launch.
+    Returns [batch, H] bf16, H = o_weight rows."""
+    batch, width = qkv.shape[0], qkv.shape[-1]
+    if qkv.numel() != batch * width or qkv.stride(-1) != 1 or qkv.dtype != torch.bfloat16:
+        raise ValueError("qkv must be a bf16 [B, 1, width] packed projection")
+    if cos.shape != sin.shape or cos.shape[-1] != _lib.HEAD_DIM or not cos.is_contiguous() \
+            or not sin.is_contiguous():
+        raise ValueError("cos/sin must be contiguous 128-wide rows")
+    _check_cache(keys, values, batch, kv_heads)
+    heads = kv_heads * groups
+    if k_offset < heads * _lib.HEAD_DIM or v_offset < k_offset + kv_heads * _lib.HEAD_DIM \
+            or v_offset + kv_heads * _lib.HEAD_DIM > width:
+        raise ValueError("k/v offsets do not fit the packed projection")
+    if positions.dtype != torch.int64:
+        raise ValueError("positions must be int64")
+    if isinstance(o_weight, QuantizedWeight):
+        data, scale, fmt = o_weight.data, o_weight.scale, o_weight.code
+    else:
+        data, scale, fmt = o_weight, None, 0
+    n = data.shape[0]
+    if data.dim() != 2 or not data.is_contiguous() or data.shape[1] != heads * _lib.HEAD_DIM:
+        raise ValueError("o_weight must be a contiguous [H, Hq * 128] weight")
+    if residual.dtype != torch.bfloat16 or residual.numel() != batch * n \
+            or not residual.is_contiguous():
+        raise ValueError("residual must be a contiguous bf16 [B, H]")
+    _lib.require_gpu(qkv, keys, values, positions, cos, sin, data, residual)
+    rope_rows = cos.numel() // _lib.HEAD_DIM
+    out = torch.empty((batch, n), dtype=qkv.dtype, device=qkv.device)
+    nbytes = _lib.load().htn_attention_output_scratch_bytes(batch, heads, kv_heads,
+                                                            keys.shape[2], n)
+    scratch = _scratch(qkv.device, batch, heads, 1, keys.shape[2], nbytes)
+    _lib.call("htn_prologue_attention_output", _lib.ptr(qkv), qkv.stride(0), k_offset, v_offset,
+              _lib.ptr(q_norm.weight), _lib.ptr(k_norm.weight), float(q_norm.variance_epsilon),
+              float(k_norm.variance_epsilon), _lib.ptr(cos), _lib.ptr(sin), _lib.HEAD_DIM,
+              rope_rows, 0, _lib.ptr(keys), _lib.ptr(values), keys.shape[2],
+              _lib.ptr(positions), batch, kv_heads, groups, _lib.ptr(data), _lib.ptr(scale),
+              fmt, n, _lib.ptr(residual), _lib.ptr(out), _lib.ptr(scratch),
+              _lib.stream(qkv.device))
     return out
 
 

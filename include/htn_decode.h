@@ -324,6 +324,12 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
  * arrival counters, is never reset by the kernels: the caller reads it (any
  * time after the calls it covers) and clears it. */
 #define HTN_ATTENTION_XCD_MISMATCH_BYTE 8
+/* Byte offset, inside the counter region, of a 32-bit count of fused
+ * output-projection blocks (htn_prologue_attention_output) that could not use
+ * their pair's attention partials: they ran on another XCD than the pair's
+ * splits, or the splits had not arrived within the wait bound. 0 on a correct
+ * run; never reset by the kernels (the caller reads and clears it). */
+#define HTN_ATTENTION_OUTPUT_ERROR_BYTE 12
 int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap);
 
 /* Grouped-query attention over fixed-capacity caches with causality by
@@ -384,6 +390,35 @@ int htn_prologue_attention_prefetch(
     int64_t cap, const int64_t* positions, void* out, int64_t B, int64_t Hkv, int64_t groups,
     void* scratch, const void* next_w, int64_t next_n, int64_t next_k, int next_format,
     htn_stream_t stream);
+
+/* htn_prologue_attention followed by the output projection with its
+ * residual: out[b, :] = bf16(bf16(W_o a[b]) + residual[b, :]) (8-bit W_o:
+ * bf16(bf16(scale_n * (W_o a)_n) + residual_n)), with a[b] the attention
+ * rows [Hq * 128] and W_o [n, Hq * 128] row-major (o_format 0 bf16, or
+ * HTN_WEIGHT_INT8 / HTN_WEIGHT_FP8_E4M3 with o_scale [n] fp32). For one
+ * sequence on the XCD-affine split grid (in-kernel merge) the projection
+ * runs in the attention launch: blocks on each kv head's XCD hold that head
+ * group's columns of W_o in registers while the attention runs, merge its
+ * rows when its last split arrives, and write fp32 partial rows; a small
+ * second launch sums the head groups' partials in a fixed order and rounds
+ * as the reference does (any summation order of the projection is the
+ * reference's contract). Otherwise the attention rows go to scratch and the
+ * residual GEMV follows. scratch holds htn_attention_output_scratch_bytes
+ * bytes, its first HTN_ATTENTION_COUNTER_BYTES zero when allocated (every
+ * call leaves them zero; a call that counted an error at
+ * HTN_ATTENTION_OUTPUT_ERROR_BYTE may not).
+ * Replaces prologue_attention(...) (kernels/attention.py:162) followed by
+ * output_projection_residual(a, W_o, residual) (kernels/projection.py:70),
+ * the pair fused_layer.py:146-147 runs. */
+int64_t htn_attention_output_scratch_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
+                                           int64_t n);
+int htn_prologue_attention_output(
+    const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off, const void* q_gain,
+    const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+    int64_t rope_st, int64_t rope_rows, int rope_by_position, void* keys, void* values,
+    int64_t cap, const int64_t* positions, int64_t B, int64_t Hkv, int64_t groups,
+    const void* o_weight, const float* o_scale, int o_format, int64_t n,
+    const void* residual, void* out, void* scratch, htn_stream_t stream);
 
 /* Diagnostics and control of the in-kernel attention merge; no counterpart
  * in the reference. htn_xcc_ids writes, for each block b < blocks of a
