@@ -21,6 +21,7 @@ HTN_ELAUNCH = -3
 HEAD_SCRATCH_BYTES = 65536
 ATTENTION_XCD_MISMATCH_BYTE = 8  # HTN_ATTENTION_XCD_MISMATCH_BYTE
 ATTENTION_OUTPUT_ERROR_BYTE = 12  # HTN_ATTENTION_OUTPUT_ERROR_BYTE
+ATTENTION_OUTPUT_ACC_BYTE = 32768  # HTN_ATTENTION_OUTPUT_ACC_BYTE
 HEAD_DIM = 128
 
 _P = ctypes.c_void_p
@@ -75,6 +76,7 @@ SIGNATURES = {
                                         _I, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _P,
                                         _I64, _I64, _I, _P],
     "htn_attention_output_scratch_bytes": [_I64, _I64, _I64, _I64, _I64],
+    "htn_attention_output_fused_calls": [],
     "htn_prologue_attention_output": [_P, _I64, _I64, _I64, _P, _P, _F, _F, _P, _P, _I64, _I64,
                                       _I, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _I, _I64,
                                       _P, _P, _P, _P],
@@ -85,7 +87,7 @@ SIGNATURES = {
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
             "htn_gemm_tiles_scratch_bytes": _I64,
             "htn_gate_up_swiglu_scratch_bytes": _I64, "htn_stream_read_blocks": _I64,
-            "htn_attention_output_scratch_bytes": _I64,
+            "htn_attention_output_scratch_bytes": _I64, "htn_attention_output_fused_calls": _I64,
             "htn_head_scratch_capacity": _I64}
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX, EPI_RESIDUAL_NORM = 0, 1, 2, 3, 4
 

@@ -39,8 +39,14 @@ constexpr int kMergeUnroll = 16;    // partials loaded back to back in the merge
 // one 128-byte line per (batch, kv head) pair, a 64-bit counter at its start.
 constexpr int kCounterStride = 32;  // uint32 words
 constexpr int kMaxCounterPairs = 256;
-constexpr long kCounterBytes = static_cast<long>(kMaxCounterPairs) * kCounterStride * 4;
+// After the counters, still in the region that starts zero and is left zero
+// by every call, the fused output projection's 64-bit row accumulators (at
+// most kOMaxRows output rows); the split partials follow the region.
+constexpr long kOAccByte = static_cast<long>(kMaxCounterPairs) * kCounterStride * 4;
+constexpr long kOMaxRows = 8192;
+constexpr long kCounterBytes = kOAccByte + kOMaxRows * 8;
 static_assert(kCounterBytes == HTN_ATTENTION_COUNTER_BYTES, "counter region size");
+static_assert(kOAccByte == HTN_ATTENTION_OUTPUT_ACC_BYTE, "accumulator offset");
 // Pair p's 64-bit counter sits at the start of its 128-byte line; the XCD
 // mismatch count is the 32-bit word right after pair 0's counter.
 constexpr long kXcdMismatchByte = HTN_ATTENTION_XCD_MISMATCH_BYTE;
@@ -53,9 +59,6 @@ constexpr long kXcdMismatchByte = HTN_ATTENTION_XCD_MISMATCH_BYTE;
 // HTN_ATTENTION_OUTPUT_ERROR_BYTE of the region counts output blocks that
 // could not use their pair's partials (another XCD, or no arrival in time).
 constexpr int kReadyLine = 128, kReadyWord = 0, kReadersWord = 1;
-// Row block q's arrival count of pair partials: counter line kSumLine + q.
-constexpr int kSumLine = kReadyLine + 8;
-constexpr int kMaxOutputBlocks = kMaxCounterPairs - kSumLine;
 constexpr long kOutputErrorByte = HTN_ATTENTION_OUTPUT_ERROR_BYTE;
 static_assert(kXcdMismatchByte >= 8 && kXcdMismatchByte + 4 <= kCounterStride * 4,
               "mismatch word inside pair 0's line, past its counter");
@@ -342,13 +345,13 @@ struct AttnArgs {
   // Output projection fused in (one sequence, in-kernel merge): o_blocks
   // blocks per pair past the attention grid, on the pair's XCD, multiply the
   // pair's columns of W_o (ow: [o_n, Hq D] bf16 or 8-bit, format o_fmt) by
-  // the pair's attention rows into fp32 partial rows ypart[pair][o_n].
+  // the pair's attention rows and add them into the row accumulators.
   const unsigned char* ow;
-  float* ypart;
+  unsigned long long* oacc;  // [o_n] row accumulators, zero between launches
   int o_fmt, o_n, o_blocks, o_lpr;
-  // The last of a row block's pair partials sums them (in pair order),
-  // applies the 8-bit row scale, rounds, adds the residual res_o and rounds
-  // into out_o: bf16(bf16(sum) + residual) (projection.py:64-67).
+  // The contribution that completes a row applies the 8-bit row scale,
+  // rounds, adds the residual res_o and rounds into out_o:
+  // bf16(bf16(sum) + residual) (projection.py:64-67).
   const float* o_scale;
   const bf16_t* res_o;
   bf16_t* out_o;
@@ -606,10 +609,8 @@ __device__ __forceinline__ void merge_row_to(const AttnArgs& a, int p, int r, in
 // loads issued at once, before the wait. When the pair's last split has
 // stored its partial, the block merges the pair's G attention rows (the
 // bf16 rows the unfused kernel writes, merge_tail's arithmetic) into LDS,
-// takes its dot products, reduces each over the 16 lanes and stores the fp32
-// row sums to ypart[p][row]. The pair's partial over its columns is summed
-// with the other pairs', scaled, rounded and added to the residual by
-// output_partials_residual.
+// takes its dot products, reduces each over the 16 lanes, and adds the row
+// sums into the rows' accumulators, where the pairs' partials meet.
 constexpr int kORowsPerGroup = 8;
 // Smallest output projection worth fusing: the fusion wins on the 8B decode
 // step (33.6 MB: 2.841 -> 2.782 ms per step), breaks even at 16.8 MB (8B int8
@@ -620,9 +621,32 @@ constexpr int kOMaxSplits = 24;
 constexpr int kORowsPerBlock = 4 * 4 * kORowsPerGroup;  // 128
 constexpr int kOMaxPolls = 1 << 16;
 
+// Adds one pair's contribution (fixed-point partial + 2^60) to output row
+// `row`'s accumulator; the contribution that completes the pair count
+// finishes the row and clears the word.
+__device__ __forceinline__ void output_row_add(const AttnArgs& a, int row,
+                                               unsigned long long add, double to_fix) {
+  const unsigned long long tot =
+      __hip_atomic_fetch_add(a.oacc + row, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+  const unsigned k = static_cast<unsigned>((tot + (1ull << 59)) >> 60);
+  if (k == static_cast<unsigned>(a.Hkv)) {
+    const long long S = static_cast<long long>(tot - (static_cast<unsigned long long>(k) << 60));
+    float sum = static_cast<float>(static_cast<double>(S) / to_fix);
+    if (a.o_scale) sum *= a.o_scale[row];
+    a.out_o[row] = static_cast<bf16_t>(f2bf(round_bf(sum) + bf2f(a.res_o[row])));
+    __hip_atomic_store(a.oacc + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <int WF, int LPR>
 __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) {
   constexpr int kB = Fmt<WF>::kBytes;
+  // Fixed point of the row partials: kFix fraction bits, |partial| < 2^(56 -
+  // kFix), so eight pairs' partials and the count in bits 60-63 cannot carry
+  // into each other.
+  constexpr int kFix = WF == WF_BF16 ? 32 : 24;
+  constexpr float kMaxPartial = static_cast<float>(1ull << (56 - kFix));
+  const double to_fix = static_cast<double>(1ull << kFix);
   constexpr int kXW = WF == WF_BF16 ? 4 : 8;  // activation words per 16-byte weight load
   const int o = static_cast<int>(blockIdx.x) - a.attn_blocks;
   const int p = o & 7, q = o >> 3;
@@ -664,12 +688,15 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
   unsigned xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
   if (rv == 0 || (rv & 0xffu) != (xcc & 0xffu)) {
-    // The partials are not visible here: leave the rows unwritten and count
-    // the failure for the host.
+    // The partials are not visible here: count the failure for the host and
+    // add only the count to the block's rows, so they complete (without this
+    // pair's share) and their accumulators are cleared as usual.
     if (threadIdx.x == 0)
       __hip_atomic_fetch_add(a.done + kOutputErrorByte / 4, 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int row = row0 + 4 * j;
+    if (j < kORowsPerGroup && row < a.o_n) output_row_add(a, row, 1ull << 60, to_fix);
     return;
   }
   // 3. The pair's attention rows into LDS, then this block is done with the
@@ -695,56 +722,40 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
 #pragma unroll
     for (int u = 0; u < kXW; ++u) x[c][u] = src[u];
   }
-  // 5. The fp32 row sums go out through cache-bypassing (agent-scope atomic)
-  // stores, so the block that completes this row block, on whichever XCD,
-  // reads them from the coherent level: the protocol of AMD's rocPRIM
-  // look-back scan on gfx942/gfx950 (atomic stores and loads of the data,
-  // order-only fences, an atomic counter), with no L2 write-back.
-  unsigned* yrow = reinterpret_cast<unsigned*>(a.ypart + static_cast<long>(p) * a.o_n);
+  // 5. Each row's partial joins the other pairs' in one 64-bit word per
+  // output row: the fp32 partial in fixed point (kFix fraction bits) plus
+  // 2^60, added by one returning agent-scope atomic, which is performed at
+  // the coherent level, so the XCDs' contributions meet without any L2
+  // write-back. Integer addition is associative: whatever the arrival
+  // order, the word ends as the exact sum of the pairs' partials, and the
+  // contribution that brings the count in bits 60-63 to the pair count
+  // sees that sum in its own return value. It finishes the row -- fp32 sum,
+  // 8-bit row scale, bf16, + residual, bf16 (projection.py:64-67) -- and
+  // clears the word for the next launch. The sum is rounded once to fp32
+  // instead of after every pair: a summation order the reference's "any
+  // order" contract allows (kernels/projection.py:25).
+  // Lane j < 8 of each group adds row it = j's sum: the group's eight
+  // returning atomics go out together.
+  float mine = 0.f;
 #pragma unroll
   for (int it = 0; it < kORowsPerGroup; ++it) {
     float s = 0.f;
 #pragma unroll
     for (int c = 0; c < LPR; ++c) s = dot_vec<WF>(w[it][c], x[c], s);
-    s = row16_sum(s);
-    const int row = row0 + 4 * it;
-    if (j == 0 && row < a.o_n)
-      __hip_atomic_store(yrow + row, __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s = row16_sum(s);  // in all 16 lanes of the group
+    if (j == it) mine = s;
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  __shared__ unsigned last_pair;
-  if (threadIdx.x == 0) {
-    unsigned* cnt = a.done + static_cast<long>(kSumLine + q) * kCounterStride;
-    const unsigned n =
-        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-    last_pair = n == static_cast<unsigned>(a.Hkv);
-    if (n == static_cast<unsigned>(a.Hkv))
-      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last_pair) return;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  // 6. This block completed row block q: every pair's partial rows are
-  // stored; sum them for rows [128 q, 128 q + 128).
-  const int t = threadIdx.x;
-  const int row = q * kORowsPerBlock + t;
-  if (t < kORowsPerBlock && row < a.o_n) {
-    const unsigned* yall = reinterpret_cast<const unsigned*>(a.ypart);
-    float v[8];
-#pragma unroll
-    for (int pp = 0; pp < 8; ++pp)
-      v[pp] = pp < a.Hkv ? __uint_as_float(__hip_atomic_load(
-                               yall + static_cast<long>(pp) * a.o_n + row, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT))
-                         : 0.f;
-    float sum = v[0];
-#pragma unroll
-    for (int pp = 1; pp < 8; ++pp) sum += v[pp];
-    if (a.o_scale) sum *= a.o_scale[row];
-    a.out_o[row] = static_cast<bf16_t>(f2bf(round_bf(sum) + bf2f(a.res_o[row])));
+  const int row = row0 + 4 * j;
+  if (j < kORowsPerGroup && row < a.o_n) {
+    if (!(fabsf(mine) < kMaxPartial)) {  // out of the fixed-point range (or NaN)
+      __hip_atomic_fetch_add(a.done + kOutputErrorByte / 4, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      mine = 0.f;
+    }
+    output_row_add(a, row,
+                   static_cast<unsigned long long>(__double2ll_rn(static_cast<double>(mine) * to_fix)) +
+                       (1ull << 60),
+                   to_fix);
   }
 }
 
@@ -2650,7 +2661,7 @@ struct FusedOutput {
   const void* w;
   long n, k;
   int format;
-  float* ypart;
+  unsigned long long* acc;
   const float* scale;
   const bf16_t* res;
   bf16_t* out;
@@ -2793,16 +2804,17 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
   // pair's span of each weight row a whole number (1, 2 or 4) of 256-byte
   // pieces and 32-bit byte offsets over the weights.
   a.ow = nullptr;
-  a.ypart = nullptr;
-  if (fo && fo->w && fo->ypart && a.done && a.ring > 0 && !a.stream && a.B == 1 && a.Q == 1 &&
+  a.oacc = nullptr;
+  if (fo && fo->w && fo->acc && a.done && a.ring > 0 && !a.stream && a.B == 1 && a.Q == 1 &&
       a.Hkv <= 8 && a.splits <= kOMaxSplits && fo->k == static_cast<long>(a.Hq) * D) {
     const long kb = fo->format == 0 ? 2 : 1;
     const long span = static_cast<long>(a.G) * D * kb;
     const long lpr = span / 256;
     if (span % 256 == 0 && (lpr == 1 || lpr == 2 || lpr == 4) && fo->n > 0 &&
-        fo->n * fo->k * kb < (1L << 31) && fo->n * fo->k * kb >= kFuseMinBytes) {
+        fo->n <= kOMaxRows && fo->n * fo->k * kb < (1L << 31) &&
+        fo->n * fo->k * kb >= kFuseMinBytes) {
       a.ow = static_cast<const unsigned char*>(fo->w);
-      a.ypart = fo->ypart;
+      a.oacc = fo->acc;
       a.o_fmt = fo->format;
       a.o_n = static_cast<int>(fo->n);
       a.o_lpr = static_cast<int>(lpr);
@@ -2811,7 +2823,6 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
       a.o_scale = fo->format != 0 ? fo->scale : nullptr;
       a.res_o = fo->res;
       a.out_o = fo->out;
-      if (a.o_blocks > kMaxOutputBlocks) a.ow = nullptr;
     }
   }
   // Prefetch of the next projection's weights: only with the XCD-affine grid
@@ -2982,23 +2993,23 @@ extern "C" int htn_prologue_attention_prefetch(
 }
 
 namespace {
-// Scratch of htn_prologue_attention_output: the attention's (counters, then
-// split partials), the fp32 partial rows of the fused output projection, and
-// the attention rows of the unfused fallback.
-long output_scratch_layout(long B, long Hq, long Hkv, long cap, long n, long* ypart_off,
-                           long* rows_off) {
-  const long base = (htn_attention_scratch_bytes(B, Hq, 1, cap) + 255) / 256 * 256;
-  *ypart_off = base;
-  *rows_off = base + (B * Hkv * n * 4 + 255) / 256 * 256;
+// Scratch of htn_prologue_attention_output: the attention's (counters and
+// the fused projection's row accumulators, then split partials), then the
+// attention rows of the unfused fallback.
+long output_scratch_layout(long B, long Hq, long cap, long* rows_off) {
+  *rows_off = (htn_attention_scratch_bytes(B, Hq, 1, cap) + 255) / 256 * 256;
   return *rows_off + B * Hq * D * 2;
 }
+
+// Calls of htn_prologue_attention_output that ran the fused projection.
+std::atomic<long> fused_output_calls{0};
 }  // namespace
 
 extern "C" int64_t htn_attention_output_scratch_bytes(int64_t B, int64_t Hq, int64_t Hkv,
                                                       int64_t cap, int64_t n) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || cap <= 0 || n <= 0) return 0;
-  long yo = 0, ro = 0;
-  return output_scratch_layout(B, Hq, Hkv, cap, n, &yo, &ro);
+  long ro = 0;
+  return output_scratch_layout(B, Hq, cap, &ro);
 }
 
 extern "C" int htn_prologue_attention_output(
@@ -3014,12 +3025,12 @@ extern "C" int htn_prologue_attention_output(
     return HTN_EINVAL;
   if (o_format != 0 && !o_scale) return HTN_EINVAL;
   const long Hq = Hkv * groups, k = Hq * D;
-  long yo = 0, ro = 0;
-  output_scratch_layout(B, Hq, Hkv, cap, n, &yo, &ro);
+  long ro = 0;
+  output_scratch_layout(B, Hq, cap, &ro);
   unsigned char* sb = static_cast<unsigned char*>(scratch);
-  float* ypart = reinterpret_cast<float*>(sb + yo);
+  unsigned long long* acc = reinterpret_cast<unsigned long long*>(sb + kOAccByte);
   bf16_t* rows = reinterpret_cast<bf16_t*>(sb + ro);
-  const FusedOutput fo{o_weight, n, k, o_format, ypart, o_scale,
+  const FusedOutput fo{o_weight, n, k, o_format, acc, o_scale,
                        static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(out)};
   // Unfused, the attention's idle CUs still prefetch W_o into L2.
   const NextWeights next{o_weight, n, k, o_format};
@@ -3028,7 +3039,10 @@ extern "C" int htn_prologue_attention_output(
                               rope_st, rope_rows, rope_by_position, keys, values, cap, positions,
                               rows, B, Hkv, groups, scratch, &next, stream, &fo, &fused);
   if (rc != HTN_OK) return rc;
-  if (fused) return HTN_OK;  // the launch wrote `out`
+  if (fused) {
+    fused_output_calls.fetch_add(1);
+    return HTN_OK;  // the launch wrote `out`
+  }
   // Unfused: the attention rows went to scratch; the residual GEMV follows.
   for (long b = 0; b < B; ++b) {
     const bf16_t* x = rows + b * k;
@@ -3040,6 +3054,8 @@ extern "C" int htn_prologue_attention_output(
   }
   return HTN_OK;
 }
+
+extern "C" int64_t htn_attention_output_fused_calls() { return fused_output_calls.load(); }
 
 extern "C" int htn_xcc_ids(int32_t* out, int64_t blocks, htn_stream_t stream) {
   if (!out || blocks <= 0 || blocks > (1L << 20)) return HTN_EINVAL;

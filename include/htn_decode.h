@@ -313,10 +313,14 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
 
 /* Bytes of scratch the attention entry points need for these sizes (for Q > 8,
  * the causal many-query kernel, only the counter region). The first
- * HTN_ATTENTION_COUNTER_BYTES hold arrival counters: zero them once when the
+ * HTN_ATTENTION_COUNTER_BYTES hold arrival counters (32 KB) and the fused
+ * output projection's row accumulators (64 KB): zero them once when the
  * buffer is allocated; every call leaves them zero. Calls sharing a scratch
  * buffer must be ordered (one stream). */
-#define HTN_ATTENTION_COUNTER_BYTES 32768
+#define HTN_ATTENTION_COUNTER_BYTES 98304
+/* Byte offset of the fused output projection's accumulators: one 64-bit
+ * word per output row (at most 8192), zero between calls. */
+#define HTN_ATTENTION_OUTPUT_ACC_BYTE 32768
 /* Byte offset, inside the counter region, of a 32-bit count of in-kernel
  * merges that found a split of their (batch, kv head) pair on another XCD
  * than their own (dispatch not round-robin, so that split's partial may not
@@ -326,9 +330,11 @@ int htn_norm_rope_cache(const void* q, int64_t q_sb, int64_t q_st, const void* k
 #define HTN_ATTENTION_XCD_MISMATCH_BYTE 8
 /* Byte offset, inside the counter region, of a 32-bit count of fused
  * output-projection blocks (htn_prologue_attention_output) that could not use
- * their pair's attention partials: they ran on another XCD than the pair's
- * splits, or the splits had not arrived within the wait bound. 0 on a correct
- * run; never reset by the kernels (the caller reads and clears it). */
+ * their pair's attention partials (they ran on another XCD than the pair's
+ * splits, or the splits had not arrived within the wait bound), plus row
+ * partials outside the fixed-point accumulator's range (|partial| >= 2^24
+ * with bf16 weights, 2^32 with 8-bit ones). 0 on a correct run; never reset
+ * by the kernels (the caller reads and clears it). */
 #define HTN_ATTENTION_OUTPUT_ERROR_BYTE 12
 int64_t htn_attention_scratch_bytes(int64_t B, int64_t Hq, int64_t Q, int64_t cap);
 
@@ -399,11 +405,14 @@ int htn_prologue_attention_prefetch(
  * sequence on the XCD-affine split grid (in-kernel merge) the projection
  * runs in the attention launch: blocks on each kv head's XCD hold that head
  * group's columns of W_o in registers while the attention runs, merge its
- * rows when its last split arrives, and write fp32 partial rows; a small
- * second launch sums the head groups' partials in a fixed order and rounds
- * as the reference does (any summation order of the projection is the
- * reference's contract). Otherwise the attention rows go to scratch and the
- * residual GEMV follows. scratch holds htn_attention_output_scratch_bytes
+ * rows when its last split arrives, and add their row sums, in 64-bit fixed
+ * point, into one accumulator word per output row (integer addition makes
+ * the total independent of the arrival order; the contribution that
+ * completes a row rounds it as the reference does -- any summation order
+ * of the projection is the reference's contract -- adds the residual and
+ * clears the word). Projections under 16 MB or over 8192 rows, and shapes
+ * the fused kernel does not cover, take the unfused path: the attention rows go to scratch
+ * and the residual GEMV follows. scratch holds htn_attention_output_scratch_bytes
  * bytes, its first HTN_ATTENTION_COUNTER_BYTES zero when allocated (every
  * call leaves them zero; a call that counted an error at
  * HTN_ATTENTION_OUTPUT_ERROR_BYTE may not).
@@ -412,6 +421,10 @@ int htn_prologue_attention_prefetch(
  * the pair fused_layer.py:146-147 runs. */
 int64_t htn_attention_output_scratch_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t cap,
                                            int64_t n);
+/* Diagnostic: how many htn_prologue_attention_output calls of this process
+ * ran the projection inside the attention launch (the rest took the
+ * unfused path). */
+int64_t htn_attention_output_fused_calls(void);
 int htn_prologue_attention_output(
     const void* qkv, int64_t qkv_sb, int64_t k_off, int64_t v_off, const void* q_gain,
     const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,

@@ -74,5 +74,7 @@ def test_header_constants_match_the_binding():
     consts = dict(re.findall(r"#define (HTN_\w+) \(?(-?\d+)\)?", text))
     assert int(consts["HTN_HEAD_SCRATCH_BYTES"]) == _lib.HEAD_SCRATCH_BYTES
     assert int(consts["HTN_ATTENTION_XCD_MISMATCH_BYTE"]) == _lib.ATTENTION_XCD_MISMATCH_BYTE
+    assert int(consts["HTN_ATTENTION_OUTPUT_ERROR_BYTE"]) == _lib.ATTENTION_OUTPUT_ERROR_BYTE
+    assert int(consts["HTN_ATTENTION_OUTPUT_ACC_BYTE"]) == _lib.ATTENTION_OUTPUT_ACC_BYTE
     assert int(consts["HTN_EINVAL"]) == _lib.HTN_EINVAL
     assert int(consts["HTN_HEAD_DIM"]) == _lib.HEAD_DIM
