@@ -348,7 +348,7 @@ struct AttnArgs {
   // the pair's attention rows and add them into the row accumulators.
   const unsigned char* ow;
   unsigned long long* oacc;  // [o_n] row accumulators, zero between launches
-  int o_fmt, o_n, o_blocks, o_lpr;
+  int o_fmt, o_n, o_blocks, o_lpr, o_delay;
   // The contribution that completes a row applies the 8-bit row scale,
   // rounds, adds the residual res_o and rounds into out_o:
   // bf16(bf16(sum) + residual) (projection.py:64-67).
@@ -624,16 +624,19 @@ constexpr int kOMaxPolls = 1 << 16;
 // Adds one pair's contribution (fixed-point partial + 2^60) to output row
 // `row`'s accumulator; the contribution that completes the pair count
 // finishes the row and clears the word.
+// `res` and `scale` are the row's residual and 8-bit row scale (1 for bf16
+// weights), loaded before the block waited.
 __device__ __forceinline__ void output_row_add(const AttnArgs& a, int row,
-                                               unsigned long long add, double to_fix) {
+                                               unsigned long long add, double to_fix, float res,
+                                               float scale) {
   const unsigned long long tot =
       __hip_atomic_fetch_add(a.oacc + row, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
   const unsigned k = static_cast<unsigned>((tot + (1ull << 59)) >> 60);
   if (k == static_cast<unsigned>(a.Hkv)) {
     const long long S = static_cast<long long>(tot - (static_cast<unsigned long long>(k) << 60));
     float sum = static_cast<float>(static_cast<double>(S) / to_fix);
-    if (a.o_scale) sum *= a.o_scale[row];
-    a.out_o[row] = static_cast<bf16_t>(f2bf(round_bf(sum) + bf2f(a.res_o[row])));
+    if (a.o_scale) sum *= scale;
+    a.out_o[row] = static_cast<bf16_t>(f2bf(round_bf(sum) + res));
     __hip_atomic_store(a.oacc + row, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -659,7 +662,7 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
   // issued about a microsecond after the attention blocks' first K/V loads
   // (8B decode step at context 2048: 2.817 -> 2.798 ms; two microseconds
   // gave 2.815).
-  __builtin_amdgcn_s_sleep(40);
+  for (int i = 0; i < a.o_delay; ++i) __builtin_amdgcn_s_sleep(40);
   const uint32_t row_bytes = static_cast<uint32_t>(a.Hq) * D * kB;
   const __amdgpu_buffer_rsrc_t wrs =
       buffer_rsrc(a.ow, static_cast<uint32_t>(a.o_n) * row_bytes);
@@ -672,6 +675,12 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
 #pragma unroll
     for (int c = 0; c < LPR; ++c) w[it][c] = buffer_load16_stream(wrs, voff + 256u * c, 0);
   }
+  // The epilogue operands of the row this lane may finish (lane j < 8 of
+  // each group: row it = j), behind the weights.
+  const int frow = row0 + 4 * j;
+  const int erow = frow < a.o_n ? frow : a.o_n - 1;
+  const float res = bf2f(a.res_o[erow]);
+  const float scale = a.o_scale ? a.o_scale[erow] : 1.f;
   // 2. Wait for the pair's splits (wave 0 polls, bounded).
   __shared__ unsigned ready;
   if (wave == 0) {
@@ -695,8 +704,7 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
       __hip_atomic_fetch_add(a.done + kOutputErrorByte / 4, 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const int row = row0 + 4 * j;
-    if (j < kORowsPerGroup && row < a.o_n) output_row_add(a, row, 1ull << 60, to_fix);
+    if (j < kORowsPerGroup && frow < a.o_n) output_row_add(a, frow, 1ull << 60, to_fix, res, scale);
     return;
   }
   // 3. The pair's attention rows into LDS, then this block is done with the
@@ -745,17 +753,16 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
     s = row16_sum(s);  // in all 16 lanes of the group
     if (j == it) mine = s;
   }
-  const int row = row0 + 4 * j;
-  if (j < kORowsPerGroup && row < a.o_n) {
+  if (j < kORowsPerGroup && frow < a.o_n) {
     if (!(fabsf(mine) < kMaxPartial)) {  // out of the fixed-point range (or NaN)
       __hip_atomic_fetch_add(a.done + kOutputErrorByte / 4, 1u, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       mine = 0.f;
     }
-    output_row_add(a, row,
+    output_row_add(a, frow,
                    static_cast<unsigned long long>(__double2ll_rn(static_cast<double>(mine) * to_fix)) +
                        (1ull << 60),
-                   to_fix);
+                   to_fix, res, scale);
   }
 }
 
@@ -2818,6 +2825,7 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
       a.o_fmt = fo->format;
       a.o_n = static_cast<int>(fo->n);
       a.o_lpr = static_cast<int>(lpr);
+      a.o_delay = 1;
       a.o_blocks = static_cast<int>((fo->n + kORowsPerBlock - 1) / kORowsPerBlock);
       a.attn_blocks = static_cast<int>(8 * a.splits);  // one pair per XCD column
       a.o_scale = fo->format != 0 ? fo->scale : nullptr;
