@@ -708,16 +708,17 @@ def run_prompt_lookup(log, shape="qwen3-8b", prompt_len=512, steps=128, seed_len
     return out
 
 
-def pmc_pass(shape="qwen3-0.6b"):
+def pmc_pass(shape="qwen3-0.6b", weight_format="bf16"):
     """Short, graph-free workload for rocprofv3 --pmc passes (counter collection
     is per dispatch, so every kernel is launched eagerly): 8 decode steps of the
     shape's workload (0.6B at context 512, 8B at context 2048 over a synthetic
-    cache), one launch of the dominant kernel per layer over the layers'
-    weights, and a 256 MiB device copy (reads and writes exactly 256 MiB) that
-    calibrates the byte counters."""
-    cfg = shape_config(shape)
+    cache; the 8B 8-bit formats at context 8192, as their bench lines), one
+    launch of the dominant kernel per layer over the layers' weights, and a
+    256 MiB device copy (reads and writes exactly 256 MiB) that calibrates the
+    byte counters."""
+    cfg = shape_config(shape, weight_format=weight_format)
     model = Qwen3Model.random(cfg)
-    ctx = 512 if shape == "qwen3-0.6b" else 2048
+    ctx = 512 if shape == "qwen3-0.6b" else (2048 if weight_format == "bf16" else 8192)
     cap = ctx + 8
     with torch.inference_mode():
         cache = D.KVCache(model, 1, cap)
@@ -740,8 +741,10 @@ def pmc_pass(shape="qwen3-0.6b"):
         dst.copy_(src)
         torch.cuda.synchronize()
     k, n2 = cfg.hidden_size, 2 * cfg.intermediate_size
-    print(json.dumps({"pmc_pass": True, "calibration_copy_bytes": src.numel() * 2,
-                      "dominant_kernel_bytes": n2 * k * 2 + k * 4 + cfg.intermediate_size * 2}),
+    print(json.dumps({"pmc_pass": True, "weight_format": weight_format, "context": ctx,
+                      "calibration_copy_bytes": src.numel() * 2,
+                      "dominant_kernel_bytes": n2 * k * (2 if weight_format == "bf16" else 1)
+                      + k * 4 + cfg.intermediate_size * 2}),
           flush=True)
 
 
@@ -804,6 +807,8 @@ def main():
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--pmc-shape", default="qwen3-8b", choices=("qwen3-0.6b", "qwen3-8b"),
                     help="model shape of the --pmc-pass workload")
+    ap.add_argument("--pmc-format", default="bf16", choices=("bf16", "int8", "fp8_e4m3"),
+                    help="projection weight format of the --pmc-pass workload (8B only)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
     ap.add_argument("--section", default="all",
@@ -820,7 +825,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_pass:
-        pmc_pass(args.pmc_shape)
+        pmc_pass(args.pmc_shape, args.pmc_format)
         return
 
     def log(msg):
