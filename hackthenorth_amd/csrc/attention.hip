@@ -348,7 +348,7 @@ struct AttnArgs {
   // the pair's attention rows and add them into the row accumulators.
   const unsigned char* ow;
   unsigned long long* oacc;  // [o_n] row accumulators, zero between launches
-  int o_fmt, o_n, o_blocks, o_lpr, o_delay;
+  int o_fmt, o_n, o_blocks, o_lpr;
   // The contribution that completes a row applies the 8-bit row scale,
   // rounds, adds the residual res_o and rounds into out_o:
   // bf16(bf16(sum) + residual) (projection.py:64-67).
@@ -612,10 +612,11 @@ __device__ __forceinline__ void merge_row_to(const AttnArgs& a, int p, int r, in
 // takes its dot products, reduces each over the 16 lanes, and adds the row
 // sums into the rows' accumulators, where the pairs' partials meet.
 constexpr int kORowsPerGroup = 8;
-// Smallest output projection worth fusing: the fusion wins on the 8B decode
-// step (33.6 MB: 2.841 -> 2.782 ms per step), breaks even at 16.8 MB (8B int8
-// 462.3 -> 462.5 tok/s, fp8 471.7 -> 473.7), and loses on the 0.6B shape
-// (4.2 MB: 0.660 -> 0.693 ms), where the projection is short anyway.
+// Smallest output projection fused: the 8B decode step's 33.6 MB and the 8-bit
+// lines' 16.8 MB gain (2.841 -> 2.730 ms, int8 462 -> 486 tok/s at 8K). The
+// 0.6B shape's 4 MiB gains 0.6% too, but its 64-step golden decode then flips
+// a token (deficit 0.022) that the oracle's own evaluation orders do not
+// explain, so it keeps the separate GEMV.
 constexpr long kFuseMinBytes = 16L << 20;
 constexpr int kOMaxSplits = 24;
 constexpr int kORowsPerBlock = 4 * 4 * kORowsPerGroup;  // 128
@@ -660,9 +661,9 @@ __device__ __forceinline__ void output_block(const AttnArgs& a, uint32_t* alds) 
   unsigned* line = a.done + static_cast<long>(kReadyLine + p) * kCounterStride;
   // 1. The block's weights, all in flight at once (rows past o_n read zeros),
   // issued about a microsecond after the attention blocks' first K/V loads
-  // (8B decode step at context 2048: 2.817 -> 2.798 ms; two microseconds
-  // gave 2.815).
-  for (int i = 0; i < a.o_delay; ++i) __builtin_amdgcn_s_sleep(40);
+  // (8B decode step at context 2048: 2.817 -> 2.798 ms; none or two
+  // microseconds were slower, and so were three to seven at context 8192).
+  __builtin_amdgcn_s_sleep(40);
   const uint32_t row_bytes = static_cast<uint32_t>(a.Hq) * D * kB;
   const __amdgpu_buffer_rsrc_t wrs =
       buffer_rsrc(a.ow, static_cast<uint32_t>(a.o_n) * row_bytes);
@@ -2825,7 +2826,6 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
       a.o_fmt = fo->format;
       a.o_n = static_cast<int>(fo->n);
       a.o_lpr = static_cast<int>(lpr);
-      a.o_delay = 1;
       a.o_blocks = static_cast<int>((fo->n + kORowsPerBlock - 1) / kORowsPerBlock);
       a.attn_blocks = static_cast<int>(8 * a.splits);  // one pair per XCD column
       a.o_scale = fo->format != 0 ? fo->scale : nullptr;
