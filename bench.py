@@ -23,10 +23,11 @@ Also on the same line:
                   against 8 TB/s;
   prefill_s, prefill_kernels
                   the captured batched prefill of the 2048-token prompt (replay
-                  time) and its matrix-core kernels at 2048 rows (the four tiled
-                  projection GEMMs and the causal attention, each over 8 layers
-                  back to back in a graph): microseconds, TFLOP/s and the
-                  fraction of the 2.5 PFLOP/s dense bf16 peak;
+                  time) and its matrix-core work at 2048 rows (the four
+                  projections -- hipBLASLt products with their row-wise
+                  epilogue launches -- and the causal attention, each over 8
+                  layers back to back in a graph): microseconds, TFLOP/s and
+                  the fraction of the 2.5 PFLOP/s dense bf16 peak;
   cpu_baseline    the CPU oracle (torch eager, this host's cores) on a bounded
                   sample of the same workload: one batched prefill of the 2048-token
                   prompt, then 32 decode steps fed the GPU's tokens, reported as
@@ -347,12 +348,13 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 
 
 def prefill_kernels(model, rows=2048, layers=8):
-    """The batched prefill's matrix-core kernels at `rows` prompt tokens: each
-    projection as the tiled GEMM launch the prefill makes (QKV store, O and
-    down + residual, gate/up + SwiGLU) and the causal attention, launched over
-    `layers` layers' weights back to back in a graph, timed with HIP events.
-    Work per launch: 2 M N K flops (N: weight rows, gate and up both counted),
-    causal attention 4 Hq D T (T + 1) / 2."""
+    """The batched prefill's matrix-core work at `rows` prompt tokens: each
+    projection as the prefill runs it (the plain product through hipBLASLt,
+    then the row-wise epilogue launch: none for QKV, SwiGLU for gate/up, the
+    residual add with the next RMSNorm for O and down) and the causal
+    attention, launched over `layers` layers' weights back to back in a graph,
+    timed with HIP events. Work per projection: 2 M N K flops (N: weight rows,
+    gate and up both counted), causal attention 4 Hq D T (T + 1) / 2."""
     from hackthenorth_amd.kernels import rows as RW
     from hackthenorth_amd.kernels.attention import grouped_attention
     c = model.config
@@ -368,9 +370,11 @@ def prefill_kernels(model, rows=2048, layers=8):
     out = {}
     for name, fn, n, k in (
             ("qkv", lambda l: RW.projection_rows(x, l.qkv_weight), sum(c.widths), h),
-            ("o_residual", lambda l: RW.residual_rows(a, l.o_weight, res), h, q_width),
+            ("o_residual", lambda l: RW.residual_norm_rows(
+                a, l.o_weight, res, l.post_attention_layernorm.weight, 1e-6), h, q_width),
             ("gate_up_swiglu", lambda l: RW.swiglu_rows(x, l.gate_up_weight), 2 * inter, h),
-            ("down_residual", lambda l: RW.residual_rows(m, l.down_weight, res), h, inter)):
+            ("down_residual", lambda l: RW.residual_norm_rows(
+                m, l.down_weight, res, l.input_layernorm.weight, 1e-6), h, inter)):
         us = graph_launch_us([lambda l=l: fn(l) for l in ls], dev)
         tflops = 2.0 * rows * n * k / us / 1e6
         out[name] = {"us": round(us, 2), "tflops": round(tflops, 1),

@@ -57,6 +57,8 @@ SIGNATURES = {
                       _P],
     "htn_gemm_tiles_scratch_bytes": [_I64, _I64, _I64, _I],
     "htn_gemm_tiles": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _P, _P],
+    "htn_gemm_library_workspace_bytes": [],
+    "htn_gemm_library": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P],
     "htn_gemm_rows_residual_norm": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F,
                                     _P, _P, _P],
     "htn_argmax_bf16": [_P, _I64, _I64, _P, _P],
@@ -86,6 +88,7 @@ SIGNATURES = {
 }
 RESTYPES = {"htn_attention_scratch_bytes": _I64, "htn_gemm_rows_scratch_bytes": _I64,
             "htn_gemm_tiles_scratch_bytes": _I64,
+            "htn_gemm_library_workspace_bytes": _I64,
             "htn_gate_up_swiglu_scratch_bytes": _I64, "htn_stream_read_blocks": _I64,
             "htn_attention_output_scratch_bytes": _I64, "htn_attention_output_fused_calls": _I64,
             "htn_head_scratch_capacity": _I64}

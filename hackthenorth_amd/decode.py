@@ -25,8 +25,8 @@ from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
 from .kernels.greedy import greedy_head
 from .kernels.projection import norm_projection, output_projection_residual
-from .kernels.rows import (greedy_rows, projection_rows, residual_norm_rows, residual_rows,
-                           splits_k, swiglu_rows)
+from .kernels.rows import (TILE_ROWS, greedy_rows, projection_rows, residual_norm_rows,
+                           residual_rows, splits_k, swiglu_rows)
 from .speculate import draft_width, verified_tokens
 
 
@@ -199,8 +199,10 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
         a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
         if multi:
             # A projection that splits K writes the next RMSNorm in its split
-            # finish; otherwise the next projection normalises its rows itself.
-            if splits_k(*layer.o_weight.shape, rows):
+            # finish, and a prompt's projections (TILE_ROWS rows or more) write
+            # it with their residual add; otherwise the next projection
+            # normalises its rows itself.
+            if rows >= TILE_ROWS or splits_k(*layer.o_weight.shape, rows):
                 r, rn = residual_norm_rows(a, layer.o_weight, h, ln2.weight,
                                            ln2.variance_epsilon)
                 m = swiglu_rows(rn, layer.gate_up_weight)
@@ -209,7 +211,7 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
                 m = swiglu_rows(r, layer.gate_up_weight, ln2.weight, ln2.variance_epsilon)
             nxt = model.layers[i + 1].input_layernorm if i + 1 < len(model.layers) \
                 else model.norm
-            if splits_k(*layer.down_weight.shape, rows):
+            if rows >= TILE_ROWS or splits_k(*layer.down_weight.shape, rows):
                 h, hn = residual_norm_rows(m, layer.down_weight, r, nxt.weight,
                                            nxt.variance_epsilon)
             else:

@@ -6,9 +6,11 @@ projections.py:168-183, kernels/gateup.py:40-58, kernels/split_down.py:85-101).
 Here every multi-row projection is one htn_gemm_rows launch (plus a K-split
 reduction when the strips alone cannot fill the GPU) with the batch-one
 GEMVs' bf16 rounding boundaries. From TILE_ROWS rows on (a prompt's
-prefill) the projections run as one tiled GEMM launch each (htn_gemm_tiles,
-both operands staged in LDS), an input RMSNorm as its own row-norm launch;
-otherwise rows run in chunks of 128.
+prefill) the plain product runs through hipBLASLt (htn_gemm_library) with
+the epilogues as row-wise launches (RMSNorm before, SwiGLU or the residual add
+with the next RMSNorm after), or, where the library has no algorithm and for
+residual projections without a following norm, as one tiled GEMM launch with
+the epilogue fused (htn_gemm_tiles); otherwise rows run in chunks of 128.
 """
 import torch
 
@@ -18,15 +20,57 @@ MAX_ROWS = 128
 TILE_ROWS = 256
 
 
+def _normed(x, gain, eps):
+    """The rows' RMSNorm with `gain` (one row-norm launch), or x without one."""
+    if gain is None:
+        return x
+    rows, k = x.shape
+    xn = torch.empty((rows, k), dtype=x.dtype, device=x.device)
+    _lib.call("htn_rms_norm", _lib.ptr(x), x.stride(0), _lib.ptr(gain), _lib.ptr(xn), rows, k,
+              float(eps), _lib.stream(x.device))
+    return xn
+
+
+def _library(x, weight, width):
+    """bf16(x W^T) for every row through hipBLASLt (htn_gemm_library), or
+    None when the library has no algorithm for the shape."""
+    rows, k = x.shape
+    lib = _lib.load()
+    out = torch.empty((rows, width), dtype=x.dtype, device=x.device)
+    workspace = torch.empty(lib.htn_gemm_library_workspace_bytes() // 16, 4, dtype=torch.float32,
+                            device=x.device)
+    rc = lib.htn_gemm_library(_lib.ptr(x), x.stride(0), _lib.ptr(weight), width, k, rows,
+                              _lib.ptr(out), out.stride(0), _lib.ptr(workspace),
+                              _lib.stream(x.device))
+    if rc == _lib.HTN_EUNSUPPORTED:
+        return None
+    _lib.check(rc, "htn_gemm_library")
+    return out
+
+
+def _prefill(x, weight, n, epilogue, gain=None, eps=1e-6):
+    """Store or SwiGLU epilogue over every row of a prompt: the plain product
+    through the library, SwiGLU as a row-wise launch; the tiled kernel when
+    the library declines the shape."""
+    xn = _normed(x, gain, eps)
+    width = 2 * n if epilogue == _lib.EPI_SWIGLU else n
+    y = _library(xn, weight, width)
+    if y is None:
+        return _tiles(xn, weight, n, epilogue)
+    if epilogue == _lib.EPI_STORE:
+        return y
+    rows = x.shape[0]
+    out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    _lib.call("htn_swiglu", _lib.ptr(y), y.stride(0), _lib.ptr(y[:, n:]), y.stride(0),
+              _lib.ptr(out), rows, n, _lib.stream(x.device))
+    return out
+
+
 def _tiles(x, weight, n, epilogue, residual=None, gain=None, eps=1e-6):
     """One htn_gemm_tiles launch over every row of x (after the rows' RMSNorm
     with `gain`, when given); returns the [M, n] output."""
     rows, k = x.shape
-    if gain is not None:
-        xn = torch.empty((rows, k), dtype=x.dtype, device=x.device)
-        _lib.call("htn_rms_norm", _lib.ptr(x), x.stride(0), _lib.ptr(gain), _lib.ptr(xn), rows, k,
-                  float(eps), _lib.stream(x.device))
-        x = xn
+    x = _normed(x, gain, eps)
     out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
     nbytes = _lib.load().htn_gemm_tiles_scratch_bytes(rows, n, k, epilogue)
     scratch = torch.empty((nbytes + 15) // 16, 4, dtype=torch.float32, device=x.device) \
@@ -71,7 +115,7 @@ def projection_rows(x, weight, gain=None, eps=1e-6):
     _check(x, weight)
     _lib.require_gpu(x, weight, gain)
     if x.shape[0] >= TILE_ROWS:
-        return _tiles(x, weight, weight.shape[0], _lib.EPI_STORE, gain=gain, eps=eps)
+        return _prefill(x, weight, weight.shape[0], _lib.EPI_STORE, gain=gain, eps=eps)
     out = torch.empty((x.shape[0], weight.shape[0]), dtype=x.dtype, device=x.device)
     for s, e in _chunks(x.shape[0]):
         _launch(x[s:e], weight, weight.shape[0], _lib.EPI_STORE, gain, eps, out=out[s:e])
@@ -116,10 +160,21 @@ def residual_norm_rows(x, weight, residual, gain, eps=1e-6):
         raise ValueError("gain must be a contiguous bf16 [N] vector")
     _lib.require_gpu(x, weight, residual, gain)
     if x.shape[0] >= TILE_ROWS:
-        out = _tiles(x, weight, n, _lib.EPI_RESIDUAL, residual=residual)
+        rows = x.shape[0]
+        y = _library(x, weight, n)
+        if y is None:
+            out = _tiles(x, weight, n, _lib.EPI_RESIDUAL, residual=residual)
+            normed = torch.empty_like(out)
+            _lib.call("htn_rms_norm", _lib.ptr(out), out.stride(0), _lib.ptr(gain),
+                      _lib.ptr(normed), rows, n, float(eps), _lib.stream(x.device))
+            return out, normed
+        # bf16(bf16(y) + residual) and its RMSNorm in one row-wise launch.
+        if not residual.is_contiguous():
+            residual = residual.contiguous()
+        out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
         normed = torch.empty_like(out)
-        _lib.call("htn_rms_norm", _lib.ptr(out), out.stride(0), _lib.ptr(gain), _lib.ptr(normed),
-                  out.shape[0], n, float(eps), _lib.stream(x.device))
+        _lib.call("htn_add_rms_norm", _lib.ptr(y), _lib.ptr(residual), _lib.ptr(gain),
+                  _lib.ptr(out), _lib.ptr(normed), rows, n, float(eps), _lib.stream(x.device))
         return out, normed
     out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
     normed = torch.empty_like(out)
@@ -141,7 +196,7 @@ def swiglu_rows(x, gate_up_weight, gain=None, eps=1e-6):
     _lib.require_gpu(x, gate_up_weight, gain)
     n = gate_up_weight.shape[0] // 2
     if x.shape[0] >= TILE_ROWS:
-        return _tiles(x, gate_up_weight, n, _lib.EPI_SWIGLU, gain=gain, eps=eps)
+        return _prefill(x, gate_up_weight, n, _lib.EPI_SWIGLU, gain=gain, eps=eps)
     out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
     for s, e in _chunks(x.shape[0]):
         _launch(x[s:e], gate_up_weight, n, _lib.EPI_SWIGLU, gain, eps, out=out[s:e])

@@ -260,6 +260,21 @@ int htn_gemm_tiles(const void* x, int64_t x_stride, const void* w, int64_t n, in
  * The two orders of the fp32 sums may round an output 1 bf16 ulp apart. */
 int64_t htn_gemm_tiles_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epilogue);
 
+/* y[m, n] = bf16(sum_k x[m, k] * w[n, k]) (fp32 accumulation) for every row
+ * m < rows, through hipBLASLt: the plain product of a prefill projection,
+ * whose epilogues (residual add with the next RMSNorm, SwiGLU) then run as
+ * htn_add_rms_norm / htn_swiglu with the same bf16 rounding boundaries as
+ * htn_gemm_tiles' fused ones. x, w, y and workspace 16-byte aligned, k and
+ * the row strides multiples of 8; workspace holds
+ * htn_gemm_library_workspace_bytes() bytes. HTN_EUNSUPPORTED when the
+ * library offers no algorithm for the shape (htn_gemm_tiles covers it).
+ * Replaces, with those epilogue launches, the reference's prefill
+ * projections (prefill.py:6-26 -> projections.py:168-183 over the prompt). */
+int64_t htn_gemm_library_workspace_bytes(void);
+int htn_gemm_library(const void* x, int64_t x_stride, const void* w, int64_t n, int64_t k,
+                     int64_t rows, void* y, int64_t y_stride, void* workspace,
+                     htn_stream_t stream);
+
 /* SwiGLU of `rows` (1..32) activation rows x[m, :k] (row stride x_stride)
  * by the interleaved K-major weight w[k, 2 * width] (row-major, w[k, 2i] the
  * gate and w[k, 2i + 1] the up weight of output i):
