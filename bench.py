@@ -811,6 +811,8 @@ def main():
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--pmc-shape", default="qwen3-8b", choices=("qwen3-0.6b", "qwen3-8b"),
                     help="model shape of the --pmc-pass workload")
+    ap.add_argument("--prefill-tiles", action="store_true",
+                    help="prompt projections on this library's tiled GEMM instead of hipBLASLt")
     ap.add_argument("--pmc-format", default="bf16", choices=("bf16", "int8", "fp8_e4m3"),
                     help="projection weight format of the --pmc-pass workload (8B only)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -828,6 +830,9 @@ def main():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         sys.exit(2)
 
+    if args.prefill_tiles:
+        from hackthenorth_amd.kernels import rows as RW
+        RW.LIBRARY = False
     if args.pmc_pass:
         pmc_pass(args.pmc_shape, args.pmc_format)
         return

@@ -18,6 +18,9 @@ from .. import _lib
 
 MAX_ROWS = 128
 TILE_ROWS = 256
+# Plain products of TILE_ROWS rows or more through hipBLASLt (False: this
+# library's tiled kernel for every prompt projection, e.g. to measure it).
+LIBRARY = True
 
 
 def _normed(x, gain, eps):
@@ -34,6 +37,8 @@ def _normed(x, gain, eps):
 def _library(x, weight, width):
     """bf16(x W^T) for every row through hipBLASLt (htn_gemm_library), or
     None when the library has no algorithm for the shape."""
+    if not LIBRARY:
+        return None
     rows, k = x.shape
     lib = _lib.load()
     out = torch.empty((rows, width), dtype=x.dtype, device=x.device)
@@ -54,7 +59,11 @@ def _prefill(x, weight, n, epilogue, gain=None, eps=1e-6):
     the library declines the shape."""
     xn = _normed(x, gain, eps)
     width = 2 * n if epilogue == _lib.EPI_SWIGLU else n
-    y = _library(xn, weight, width)
+    # A plain store of under 512 rows keeps the tiles' k split: the 8B QKV
+    # projection at 256 rows takes 35.5 us there against 42.4 us through the
+    # library (which wins from 512 rows on and for every other projection).
+    y = _library(xn, weight, width) if epilogue != _lib.EPI_STORE or x.shape[0] >= 2 * TILE_ROWS \
+        else None
     if y is None:
         return _tiles(xn, weight, n, epilogue)
     if epilogue == _lib.EPI_STORE:
