@@ -2331,19 +2331,30 @@ __global__ __launch_bounds__(HPB * kBlock) void attention_prefill(AttnArgs a) {
       issue_vt_tr<8192>(va, vw[2]);
       issue_vt_tr<12288>(va, vw[3]);
       // Scores in base 2; slots past the query's position masked unless the
-      // whole tile is visible to every query of the wave.
-      const bool all_visible = s0 + kSplit - 1 <= wave_first;
+      // whole tile is visible to every query of the wave (a wave-uniform
+      // branch: the mask is computed only on the tiles that need it).
       float sc[4][4];
       float tmax = -INFINITY;
+      if (__builtin_expect(s0 + kSplit - 1 <= wave_first, 1)) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = st[mt][i] * scale2;
-          if (!all_visible) v = s0 + 16 * mt + 4 * quad + i <= pos ? v : -INFINITY;
-          sc[mt][i] = v;
-          tmax = fmaxf(tmax, v);
-        }
+          for (int i = 0; i < 4; ++i) {
+            sc[mt][i] = st[mt][i] * scale2;
+            tmax = fmaxf(tmax, sc[mt][i]);
+          }
+      } else {
+        // Slot s0 + 16 mt + 4 quad + i is visible iff 16 mt + i <= lim.
+        const int lim = pos - s0 - 4 * quad;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = st[mt][i] * scale2;
+            sc[mt][i] = 16 * mt + i <= lim ? v : -INFINITY;
+            tmax = fmaxf(tmax, sc[mt][i]);
+          }
+      }
       tmax = quad_max(tmax);
       const float m_new = fmaxf(m, tmax);
       // A query with nothing visible yet keeps weight 0 (no inf - inf).
