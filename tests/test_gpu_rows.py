@@ -114,6 +114,38 @@ def _tiles_abi(x, w, n, epilogue, residual=None, split=True):
 # projection at 256 and 300 rows, a 4B-wide O projection, a ragged width);
 # at 1024 rows the 8B O and down projections take 128-row tiles whose count
 # equals the 256 CUs, and split each tile's k range in two.
+LIBRARY_CASES = [(2048, 4096, 4096), (2048, 4096, 12288), (512, 4096, 4096), (1024, 4096, 12288),
+                 (300, 2560, 2560), (777, 1000, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", LIBRARY_CASES)
+def test_library_projection_matches_oracle_and_keeps_its_bits(m, n, k):
+    """htn_gemm_library picks its algorithm on a shape's first call (timing
+    only the candidates whose output equals the heuristic's first); the
+    first call, later calls and a graph replay give the same bits, within
+    one bf16 ulp of the oracle."""
+    w = nrm(48, (n, k), std=0.02)
+    x = nrm(49, (m, k))
+    wd, xd = w.cuda(), x.cuda()
+    with torch.inference_mode():
+        first = RW._library(xd, wd, n)
+        if first is None:
+            pytest.skip("no library algorithm for this shape")
+        again = RW._library(xd, wd, n)
+        assert torch.equal(first, again)
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            captured = RW._library(xd, wd, n)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(captured, first)
+            assert torch.equal(RW._library(xd, wd, n), first)
+    within_one_ulp(first, Q.linear(x, w))
+
+
 SPLIT_CASES = [(256, 4096, 12288), (300, 2560, 4096), (260, 1000, 2048),
                (1024, 4096, 4096), (1024, 4096, 12288)]
 
