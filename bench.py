@@ -752,6 +752,44 @@ def pmc_pass(shape="qwen3-0.6b", weight_format="bf16"):
           flush=True)
 
 
+def pmc_pass_rows(workload):
+    """Graph-free multi-row workloads for the same counter passes: "prefill"
+    runs the 8B 2048-token prompt's batched forward twice (the first call of
+    each library GEMM shape picks its algorithm; the second pass is the one
+    to read), "rows" eight batched decode steps of 16 sequences at context
+    512 (the multi-row MFMA projections and the per-sequence attention); both
+    end with the 256 MiB calibration copy."""
+    cfg = shape_config("qwen3-8b")
+    model = Qwen3Model.random(cfg)
+    dev = model.device
+    with torch.inference_mode():
+        if workload == "prefill":
+            rows, batch = 2048, 1
+            cache = D.KVCache(model, 1, rows + 8)
+            rotary = D.RotaryTable(model, rows + 8)
+            ids = DR.randint(rows, cfg.vocab_size, 5, 1, device=dev).view(1, rows)
+            pos = torch.arange(rows, dtype=torch.int64, device=dev)
+            for _ in range(2):
+                D.forward(model, ids, cache, pos, rotary=rotary)
+        else:
+            rows, batch, ctx = 16, 16, 512
+            cache = D.KVCache(model, batch, ctx + 8)
+            DR.normal_(cache.storage.view(-1), 21, 78, 1.0)
+            rotary = D.RotaryTable(model, ctx + 8)
+            ids = torch.zeros((batch, 1), dtype=torch.int64, device=dev)
+            for i in range(8):
+                pos = torch.full((1,), ctx + i, dtype=torch.int64, device=dev)
+                ids = D.forward(model, ids, cache, pos, rotary=rotary)
+        src = torch.empty(128 << 20, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        DR.normal_(src, 9, 9, 1.0)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": True, "workload": workload, "rows": rows, "batch": batch,
+                      "calibration_copy_bytes": src.numel() * 2}), flush=True)
+
+
 def decode_line(res):
     """The common keys of a decode result."""
     return {"tok_s": round(res["tok_s"], 2), "ms_per_step": round(res["ms_per_step"], 4),
@@ -817,6 +855,9 @@ def main():
                     help="projection weight format of the --pmc-pass workload (8B only)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
+    ap.add_argument("--pmc-workload", default="decode", choices=("decode", "prefill", "rows"),
+                    help="workload of --pmc-pass: decode steps (default), the 8B 2048-token "
+                         "prefill, or 8B batched decode at 16 rows")
     ap.add_argument("--section", default="all",
                     choices=("all", "qwen3-0.6b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
                              "batched", "per-op", "prefill", "cfg1", "prompt-lookup"),
@@ -834,7 +875,10 @@ def main():
         from hackthenorth_amd.kernels import rows as RW
         RW.LIBRARY = False
     if args.pmc_pass:
-        pmc_pass(args.pmc_shape, args.pmc_format)
+        if args.pmc_workload == "decode":
+            pmc_pass(args.pmc_shape, args.pmc_format)
+        else:
+            pmc_pass_rows(args.pmc_workload)
         return
 
     def log(msg):
