@@ -757,9 +757,10 @@ def pmc_pass_rows(workload):
     runs the 8B 2048-token prompt's batched forward twice (the first call of
     each library GEMM shape picks its algorithm; the second pass is the one
     to read), "rows" eight batched decode steps of 16 sequences at context
-    512 (the multi-row MFMA projections and the per-sequence attention); both
-    end with the 256 MiB calibration copy."""
-    cfg = shape_config("qwen3-8b")
+    512 (the multi-row MFMA projections and the per-sequence attention),
+    "verify" eight 5-row verify passes of the 4B shape at context 4096 (the
+    speculative target's pass); all end with the 256 MiB calibration copy."""
+    cfg = shape_config("qwen3-4b" if workload == "verify" else "qwen3-8b")
     model = Qwen3Model.random(cfg)
     dev = model.device
     with torch.inference_mode():
@@ -771,6 +772,15 @@ def pmc_pass_rows(workload):
             pos = torch.arange(rows, dtype=torch.int64, device=dev)
             for _ in range(2):
                 D.forward(model, ids, cache, pos, rotary=rotary)
+        elif workload == "verify":
+            rows, batch, ctx = 5, 1, 4096
+            cache = D.KVCache(model, 1, ctx + 48)
+            DR.normal_(cache.storage.view(-1), 21, 79, 1.0)
+            rotary = D.RotaryTable(model, ctx + 48)
+            ids = torch.zeros((1, rows), dtype=torch.int64, device=dev)
+            for i in range(8):
+                pos = torch.arange(ctx + 5 * i, ctx + 5 * i + rows, dtype=torch.int64, device=dev)
+                D.forward(model, ids, cache, pos, last_only=False, rotary=rotary)
         else:
             rows, batch, ctx = 16, 16, 512
             cache = D.KVCache(model, batch, ctx + 8)
@@ -855,9 +865,10 @@ def main():
                     help="projection weight format of the --pmc-pass workload (8B only)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for rocprofv3 counter passes (no JSON bench line)")
-    ap.add_argument("--pmc-workload", default="decode", choices=("decode", "prefill", "rows"),
+    ap.add_argument("--pmc-workload", default="decode",
+                    choices=("decode", "prefill", "rows", "verify"),
                     help="workload of --pmc-pass: decode steps (default), the 8B 2048-token "
-                         "prefill, or 8B batched decode at 16 rows")
+                         "prefill, 8B batched decode at 16 rows, or the 4B 5-row verify pass")
     ap.add_argument("--section", default="all",
                     choices=("all", "qwen3-0.6b", "qwen3-8b-int8", "qwen3-8b-fp8", "speculative",
                              "batched", "per-op", "prefill", "cfg1", "prompt-lookup"),
