@@ -270,10 +270,11 @@ int64_t htn_gemm_tiles_scratch_bytes(int64_t rows, int64_t n, int64_t k, int epi
  * library offers no algorithm for the shape (htn_gemm_tiles covers it).
  * The first call for a shape outside stream capture also picks the
  * algorithm: it times the library's candidates whose output equals the
- * heuristic's first (bit for bit, on the call's operands) and keeps the
- * fastest, so results never depend on the pick; that call allocates a
- * temporary copy of y and synchronises the stream. Calls under capture
- * before it use the heuristic's first algorithm.
+ * heuristic's first (bit for bit, on the call's operands), each with its
+ * weights from HBM, and keeps the fastest if it beats the first by at least
+ * 5%, so results never depend on the pick; that call allocates about 512 MB
+ * plus a copy of y for the duration, and synchronises the stream. Calls
+ * under capture before it use the heuristic's first algorithm.
  * Replaces, with those epilogue launches, the reference's prefill
  * projections (prefill.py:6-26 -> projections.py:168-183 over the prompt). */
 int64_t htn_gemm_library_workspace_bytes(void);
