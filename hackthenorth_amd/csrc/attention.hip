@@ -2785,11 +2785,15 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
     // LDS per block: 32 KB per staged tile plus up to 19 KB (8 rows) of
     // state; two-tile rings fit two blocks per CU for rows <= 4. Between one
     // and two single-tile blocks per CU the register kernel below was
-    // measured faster (8B shape, 2K context).
+    // measured faster (8B shape, 2K context). Three or more query rows per
+    // kv head score and weigh on the matrix cores here too (8B, 16 sequences
+    // at context 512: 4.39 -> 4.28 ms per step; one tile more or fewer per
+    // block measured slower, 4.31 / 4.33 ms).
     const long per_cu = rows <= 4 ? 2 : 1;
     long nt = 1;
     if (heads * tiles > 2 * cus) nt = (heads * tiles + per_cu * cus - 1) / (per_cu * cus);
     a.ring = nt == 1 ? 1 : (per_cu == 2 || nt < 4 ? 2 : 4);
+    a.mfma = rows >= 3;
     split = nt * kSplit;
   } else if (rows <= 4 && tiles >= 4 * per_head) {
     const long t = 2 * (tiles / (2 * per_head));  // even tile count

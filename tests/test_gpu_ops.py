@@ -261,7 +261,9 @@ def test_norm_rope_cache_ragged_head_counts(q_heads, kv_heads):
 ATTN_CASES = [(1, 1, 0, 129), (1, 4, 63, 513), (4, 4, 126, 257), (1, 1, 2047, 2304),
               (1, 5, 4091, 4100), (2, 1, 700, 8200),
               # one query per sequence: a tile boundary, batches, the last slot
-              (1, 1, 15, 129), (3, 1, 500, 513), (1, 1, 1023, 1024), (2, 1, 700, 1000)]
+              (1, 1, 15, 129), (3, 1, 500, 513), (1, 1, 1023, 1024), (2, 1, 700, 1000),
+              # many (sequence, kv head) pairs, several tiles per block (batched decode)
+              (16, 1, 519, 520), (8, 1, 2047, 2048)]
 
 
 @pytest.mark.parametrize("batch,queries,first,capacity", ATTN_CASES)
