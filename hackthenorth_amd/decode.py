@@ -19,7 +19,7 @@ import torch
 
 from ._lib import HEAD_DIM
 from .kernels.attention import (check_xcd_merge, decode_attention, grouped_attention,
-                                prologue_attention_output)
+                                prologue_attention, prologue_attention_output)
 from .kernels.down import down_residual
 from .kernels.embed import embed_gather, embed_gather_pair
 from .kernels.fused import norm_rope_cache
@@ -191,12 +191,21 @@ def _forward_rows(model, token_ids, cache, positions, last_only, position_embedd
         else:
             packed = torch.stack([norm_projection(h[r], ln1.weight, layer.qkv_weight,
                                                   ln1.variance_epsilon) for r in range(rows)])
-        q, k, v = packed.view(b, t, -1).split(widths, -1)
-        shape = (b, t, -1, c.head_dim)
-        q, _, _ = norm_rope_cache(q.view(shape), k.view(shape), v.view(shape), layer.q_norm,
-                                  layer.k_norm, cos, sin, cache.keys[i], cache.values[i],
-                                  positions)
-        a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
+        if t == 1 and positions.numel() == 1:
+            # One token per sequence at one shared position (batched decode):
+            # QK-norm, RoPE and the K/V append inside the attention launch,
+            # with norm_rope_cache's per-head arithmetic (bit-identical).
+            a = prologue_attention(packed.view(b, 1, -1), layer.q_norm, layer.k_norm, cos, sin,
+                                   cache.keys[i], cache.values[i], positions,
+                                   c.num_key_value_heads, groups, widths[0],
+                                   widths[0] + widths[1]).view(b, -1)
+        else:
+            q, k, v = packed.view(b, t, -1).split(widths, -1)
+            shape = (b, t, -1, c.head_dim)
+            q, _, _ = norm_rope_cache(q.view(shape), k.view(shape), v.view(shape), layer.q_norm,
+                                      layer.k_norm, cos, sin, cache.keys[i], cache.values[i],
+                                      positions)
+            a = _attention_chunks(q, cache.keys[i], cache.values[i], positions, groups)
         if multi:
             # A projection that splits K writes the next RMSNorm in its split
             # finish, and a prompt's projections (TILE_ROWS rows or more) write

@@ -443,6 +443,30 @@ def test_prologue_attention_matches_separate_ops_with_poisoned_tail(capacity, po
         assert bits_equal(row, actual.cpu())
 
 
+@pytest.mark.parametrize("batch,capacity,position", [(3, 640, 600), (16, 520, 515), (8, 2100, 2047)])
+def test_prologue_attention_batched_matches_separate_ops(batch, capacity, position):
+    """One token per sequence at one shared position (the batched decode
+    step): the fused prologue over a batch equals norm_rope_cache then
+    grouped_attention bit for bit, cache rows included."""
+    qg, kg = _norm(nrm(43, (128,))), _norm(nrm(44, (128,)))
+    cos_t, sin_t = (cuda(t) for t in Q.rope_tables(capacity, 128, 1e6))
+    p = position
+    packed = cuda(nrm(45, (batch, 1, 6144)))
+    keys = cuda(nrm(46, (batch, 8, capacity, 128)))
+    values = cuda(nrm(47, (batch, 8, capacity, 128)))
+    keys[:, :, p:] = float("nan")
+    values[:, :, p:] = float("nan")
+    ek, ev = keys.clone(), values.clone()
+    pos = torch.tensor([p], dtype=torch.int64, device="cuda")
+    q, k, v = (t.view(batch, 1, -1, 128) for t in packed.split((4096, 1024, 1024), -1))
+    cos, sin = cos_t[p:p + 1][None], sin_t[p:p + 1][None]
+    rq, _, _ = F.norm_rope_cache(q, k, v, qg, kg, cos, sin, ek, ev, pos)
+    expected = A.grouped_attention(rq, ek, ev, pos)
+    actual = A.prologue_attention(packed, qg, kg, cos, sin, keys, values, pos, 8, 4, 4096, 5120)
+    assert bits_equal(actual, expected.cpu())
+    assert bits_equal(keys, ek.cpu()) and bits_equal(values, ev.cpu())
+
+
 def test_captured_graph_replays_track_changed_inputs():
     torch.manual_seed(0)
     n, k = 6144, 1024
