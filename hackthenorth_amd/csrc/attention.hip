@@ -2781,14 +2781,16 @@ int run_attention(bool fused, AttnArgs& a, void* scratch, hipStream_t st,
     a.ring = nt == 1 ? 1 : 2;
     a.mfma = 1;
     split = nt * kSplit;
-  } else if (a.Q == 1 && rows <= 8 && (heads * tiles <= cus || heads * tiles > 2 * cus)) {
+  } else if (a.Q == 1 && rows <= 8 &&
+             (heads * tiles <= cus || heads * tiles > 2 * cus || rows >= 3)) {
     // LDS per block: 32 KB per staged tile plus up to 19 KB (8 rows) of
     // state; two-tile rings fit two blocks per CU for rows <= 4. Between one
     // and two single-tile blocks per CU the register kernel below was
-    // measured faster (8B shape, 2K context). Three or more query rows per
-    // kv head score and weigh on the matrix cores here too (8B, 16 sequences
-    // at context 512: 4.39 -> 4.28 ms per step; one tile more or fewer per
-    // block measured slower, 4.31 / 4.33 ms).
+    // measured faster for two rows per kv head (8B shape, 2K context). Three
+    // or more query rows per kv head score and weigh on the matrix cores here
+    // (8B, 16 sequences at context 512: 4.39 -> 4.28 ms per step, one tile
+    // more or fewer per block measured slower, 4.31 / 4.33 ms; 4 sequences,
+    // between one and two blocks per CU: 3.55 -> 3.52 ms).
     const long per_cu = rows <= 4 ? 2 : 1;
     long nt = 1;
     if (heads * tiles > 2 * cus) nt = (heads * tiles + per_cu * cus - 1) / (per_cu * cus);
