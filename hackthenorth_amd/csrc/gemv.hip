@@ -483,6 +483,14 @@ int dispatch(GemvArgs& a, hipStream_t st) {
   }
   if (chunks <= 2) {
     if (S == 1 && many_rows) return launch_vec<4, S, 2, NORM, EPI, WF>(a, st);
+    if constexpr (NORM && WF == WF_BF16) {
+      // RMSNorm projections of rows this short (the 0.6B QKV and gate/up,
+      // 2 KB rows) take four rows or row pairs per wave whenever every CU
+      // still gets a block, so a CU keeps 64 KB in flight instead of 16
+      // (0.6B step 0.662 -> 0.643 ms; one row pair more or fewer, or eight
+      // rows, measured slower).
+      if (a.n >= 4L * device_cus()) return launch_vec<4, S, 2, NORM, EPI, WF>(a, st);
+    }
     return launch_vec<1, S, 2, NORM, EPI, WF>(a, st);
   }
   if (chunks <= 4) return launch_vec<1, S, 4, NORM, EPI, WF>(a, st);
