@@ -218,6 +218,28 @@ def test_0p6b_decode_at_context_512_teacher_forced():
     record_sequence(oracle, prompt, emitted, "0.6b ctx 512, 64 steps")
 
 
+def test_8b_full_depth_decode_teacher_forced():
+    """All 36 layers of the 8B shape (random weights, full vocabulary): a
+    256-token prompt through the batched prefill (library products), then 16
+    steps of the captured decode graph (fused attention + output projection),
+    every emitted token teacher-forced against the oracle's 36-layer pass."""
+    shape = Q.SHAPES["8b"]
+    prompt_len, steps = 256, 16
+    prompt = Q.prompt_ids(prompt_len, shape.vocab)
+    model = Qwen3Model.random(shape_config("qwen3-8b"))
+    from hackthenorth_amd.kernels import attention as A
+    A.xcd_merge_mismatches(reset=True)
+    with torch.inference_mode():
+        state = D.DecodeState(model, 1, prompt_len, steps)
+        first = prefill(model, state, torch.tensor([prompt], device="cuda"))[:, 0].tolist()
+        emitted = [t[0] for t in D.stream_decode(state, first, steps)]
+    assert A.xcd_merge_mismatches() == 0
+    del state, model
+    torch.cuda.empty_cache()
+    oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), prompt_len + steps)
+    record_sequence(oracle, prompt, emitted, "8b full depth, prompt 256, 16 steps")
+
+
 def test_8b_prefill_2048_matches_oracle_batched_forward():
     """The captured batched prefill of a 2048-token prompt (two 8B layers):
     per layer on identical inputs, every prompt slot's K/V and every row of
