@@ -316,6 +316,32 @@ def test_draft_speculation_emits_oracle_greedy_ids(draft_seed, k):
     print(f"{same}/{steps} ids equal to the oracle's free-running greedy decode", flush=True)
 
 
+@pytest.mark.parametrize("draft_name", ["self", "0.6b"])
+def test_4b_full_depth_draft_speculation_teacher_forced(draft_name):
+    """Draft-model speculation with the 4B target at full depth (36 layers,
+    full vocabulary), k = 4: a copy of the target as its own draft (most
+    proposals accepted, so the verify pass's later rows emit tokens; the
+    draft's one-row steps and the verify pass's rows round apart at
+    random-weight near-ties, which rejects the rest) and the 0.6B shape as
+    the draft (proposals rejected, the verify pass's first row emits); every
+    emitted token teacher-forced against the oracle's 4B pass."""
+    shape = Q.SHAPES["4b"]
+    prompt_len, steps = 64, 24
+    prompt = Q.prompt_ids(prompt_len, shape.vocab)
+    target = Qwen3Model.random(shape_config("qwen3-4b"))
+    draft = Qwen3Model.random(shape_config("qwen3-4b" if draft_name == "self" else "qwen3-0.6b"))
+    spec = DraftSpeculator(target, draft, prompt_len, steps, draft_tokens=4)
+    got = [t[0] for t in spec.generate(prompt, steps)]
+    acceptance = spec.acceptance
+    del spec, target, draft
+    torch.cuda.empty_cache()
+    if draft_name == "self":
+        assert acceptance > 0.5, acceptance
+    oracle = Q.Oracle(shape, Q.generate_weights(shape, seed=0), prompt_len + steps)
+    record_sequence(oracle, prompt, got, f"4b full depth, {draft_name} draft, k 4 (acceptance "
+                                         f"{acceptance:.2f})")
+
+
 @pytest.mark.parametrize("shape_name,batch,prompt_len,steps",
                          [("tiny", 4, 9, 16), ("tiny", 16, 9, 16), ("0.6b", 4, 32, 16)])
 def test_engine_generate_batched_teacher_forced(tmp_path, shape_name, batch, prompt_len, steps):
